@@ -1,0 +1,201 @@
+#!/usr/bin/env python3
+"""Benchmark of the MoE routed-expert hot path on one MI355X.
+
+Headline: fused TopK+softmax, radix branch,
+fp32 logits [64, 32768], K = 2048.  A step is one topk_softmax call on
+inputs already resident in HBM; ``value`` is algorithmic HBM bytes per call
+(logits read + fp32 scores + int32 indices written = 9,437,184 B) divided
+by the measured time per call, in GB/s.
+
+The other BASELINE configurations are measured after the headline and
+reported under "secondary" (router C1/C3a/C3b in us and GB/s, grouped GEMM
+C4/C5 in TFLOP/s with %MFMA and %HBM).  ``cpu_baseline`` is the reference's
+CPU PyTorch path (torch.topk + softmax, kernels/topk_softmax_baseline.py:39-66)
+timed on this host's cores on the same C2 input.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only c2|c5|...]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--only", default="", help="comma list of c1,c2,c3a,c3b,c4,c5 (profiling runs)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                     "profiles", "traffic_radix_topk_c2.json"),
+                   help="rocprofv3 --pmc summary giving measured HBM bytes per radix launch")
+    return p.parse_args()
+
+
+def gpu_time_ms(fn, steps: int, warmup: int) -> float:
+    """Average ms per call of fn over `steps` calls, HIP events on the stream
+    the kernels are launched on (torch's current stream)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def router_bytes(M, N, K, in_bytes):
+    return M * N * in_bytes + M * K * 4 + M * K * 4
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the router shards rows and the GEMM shards experts with no exchange "
+              "inside the measured kernels); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from tilelang_moe_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    only = set(filter(None, args.only.split(",")))
+    want = (lambda c: not only or c in only)
+    secondary = {}
+
+    # ---------------- headline: C2 radix router ----------------
+    g = torch.Generator().manual_seed(0)
+    x2_cpu = torch.randn(64, 32768, generator=g)
+    x2 = x2_cpu.to(dev)
+    b2 = router_bytes(64, 32768, 2048, 4)
+    ms2 = None
+    if want("c2"):
+        ms2 = gpu_time_ms(lambda: K.topk_softmax(x2, 2048), args.steps, args.warmup)
+
+    # ---------------- secondary router configs ----------------
+    router_cfgs = {
+        "c1": ("topk_softmax fp32 [320,128] K=6 (selection)", 320, 128, 6, False),
+        "c3a": ("topk_softmax bf16 [4096,64] K=6 (bitonic)", 4096, 64, 6, True),
+        "c3b": ("topk_softmax bf16 [4096,256] K=8 (selection)", 4096, 256, 8, True),
+    }
+    for name, (desc, M, N, Kk, bf16) in router_cfgs.items():
+        if not want(name):
+            continue
+        x = torch.randn(M, N, generator=torch.Generator().manual_seed(0))
+        x = (x.bfloat16() if bf16 else x).to(dev)
+        ms = gpu_time_ms(lambda: K.topk_softmax(x, Kk), args.steps, args.warmup)
+        nb = router_bytes(M, N, Kk, 2 if bf16 else 4)
+        secondary[name] = {"workload": desc, "algo": K.select_strategy(N, Kk), "us": ms * 1e3,
+                           "GB_s": nb / ms / 1e6, "frac_hbm": nb / ms / 1e6 / HBM_PEAK_GBS}
+
+    # ---------------- grouped GEMM configs ----------------
+    def gemm_cfg(name, desc, T, H, I, E, topk, skew):
+        gg = torch.Generator().manual_seed(0)
+        if skew:
+            bias = 1.5 * torch.randn(E, generator=gg)
+            idx = torch.topk(torch.randn(T, E, generator=gg) + bias, topk).indices
+        else:
+            idx = torch.topk(torch.randn(T, E, generator=gg), topk).indices
+        gc = torch.Generator(device=dev).manual_seed(0)
+        X = torch.randn(T, H, generator=gc, device=dev).bfloat16()
+        W = torch.empty(E, I, H, dtype=torch.bfloat16, device=dev)
+        for e0 in range(0, E, 32):
+            e1 = min(E, e0 + 32)
+            W[e0:e1] = (0.02 * torch.randn(e1 - e0, I, H, generator=gc, device=dev)).bfloat16()
+        idx = idx.to(dev)
+        steps = max(5, min(args.steps, 50 if skew else args.steps))
+        ms = gpu_time_ms(lambda: K.grouped_gemm(X, W, idx), steps, min(args.warmup, 5))
+        R = T * topk
+        flops = 2.0 * R * H * I
+        e_nz = int((torch.bincount(idx.flatten(), minlength=E) > 0).sum())
+        nbytes = e_nz * I * H * 2 + T * H * 2 + R * I * 2 + R * 4
+        tf = flops / ms / 1e9
+        secondary[name] = {"workload": desc, "ms": ms, "TFLOP_s": tf, "frac_mfma": tf / BF16_PEAK_TFLOPS,
+                           "GB_s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+                           "rows": R, "experts_nonempty": e_nz}
+        del W, X
+
+    if want("c4"):
+        gemm_cfg("c4", "grouped_gemm bf16 T=4096 H=1024 I=256 E=8 top-2 (8192 rows)", 4096, 1024, 256, 8, 2, False)
+    if want("c5"):
+        gemm_cfg("c5", "grouped_gemm bf16 T=4096 H=7168 I=2048 E=256 top-8 skewed (32768 rows)",
+                 4096, 7168, 2048, 256, 8, True)
+
+    # ---------------- CPU baseline (reference torch path) ----------------
+    cpu = None
+    if not args.no_cpu and ms2 is not None:
+        from oracle import torch_baseline as tb
+        threads = torch.get_num_threads()
+        tb.topk_softmax_fused(x2_cpu, 2048)  # warm-up
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 10.0:
+            tb.topk_softmax_fused(x2_cpu, 2048)
+            n += 1
+        cpu_ms = (time.perf_counter() - t0) / n * 1e3
+        cpu = {"value": b2 / cpu_ms / 1e6, "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"{n} calls of torch.topk+softmax on the C2 fp32 [64,32768] K=2048 input "
+                         f"({cpu_ms:.3f} ms/call, {cpu_model()}, torch {torch.__version__})"}
+
+    if ms2 is None:
+        print(json.dumps({"secondary": secondary}))
+        return
+
+    achieved = b2 / ms2 / 1e6
+    traffic = None
+    if os.path.exists(args.traffic):
+        try:
+            traffic = json.load(open(args.traffic)).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    out = {
+        "metric": "router us + HBM GB/s; grouped-GEMM TFLOP/s (% bf16 MFMA peak), 1 MI355X",
+        "value": achieved,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms2,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) logits)",
+        "config": {"workload": "topk_softmax radix, fp32 logits [64,32768], K=2048 (BASELINE configs[1])",
+                   "M": 64, "N": 32768, "K": 2048, "us_per_call": ms2 * 1e3},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,157 @@
+/*
+ * moe_hip.h — C ABI of the MI355X (gfx950) MoE routed-expert hot path.
+ *
+ * The reference (Wendy-Hamlet/tilelang_moe) has no FFI: its boundary is the
+ * Python API in kernels/__init__.py, whose two hot-path names are
+ *   topk_softmax  = topk_softmax_best   (kernels/__init__.py:21,
+ *                                        kernels/topk_softmax_tilelang.py:1103-1135)
+ *   grouped_gemm  = grouped_gemm_best   (kernels/__init__.py:34,
+ *                                        kernels/grouped_gemm_tilelang.py:859-890)
+ * This library is what those Python functions call in this build (through
+ * ctypes, see tilelang_moe_amd/_lib.py).  Every entry point below cites the
+ * reference function it replaces.
+ *
+ * Conventions shared by every entry point:
+ *   - All data pointers are DEVICE pointers.  `stream` is a hipStream_t
+ *     (pass torch.cuda.current_stream().cuda_stream, or NULL for the
+ *     default stream).  Nothing here synchronises the stream, allocates or
+ *     frees device memory.
+ *   - Return value: 0 on success, a negative MOE_E* code on failure; the
+ *     message of the last failure on the calling thread is moe_last_error().
+ *   - Workspaces are caller-owned device buffers of at least the size the
+ *     matching *_workspace_size() function returns.  A workspace must be
+ *     all-zero before its first use; every entry point leaves it all-zero
+ *     again when it returns successfully, so a workspace can be reused by
+ *     consecutive calls on ONE stream.  Calls that overlap in time must use
+ *     different workspaces.
+ */
+#ifndef MOE_HIP_H
+#define MOE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types understood by the entry points. */
+enum moe_dtype {
+  MOE_F32 = 0,
+  MOE_BF16 = 1,
+  MOE_F16 = 2,
+  MOE_I32 = 3,
+  MOE_I64 = 4
+};
+
+/* Router algorithms (argument `algo` of moe_topk_softmax). */
+enum moe_topk_algo {
+  MOE_TOPK_AUTO = -1,      /* N<=64 bitonic, 65..512 selection, >512 radix */
+  MOE_TOPK_BITONIC = 0,    /* wave64 register bitonic network, N <= 64     */
+  MOE_TOPK_SELECTION = 1,  /* K rounds of wave64 argmax, N <= 1024         */
+  MOE_TOPK_RADIX = 2       /* multi-pass radix select, any N, K <= 16384   */
+};
+
+/* Error codes. */
+#define MOE_OK 0
+#define MOE_EINVAL (-1)   /* bad shape, dtype, pointer or alignment        */
+#define MOE_EUNSUP (-2)   /* valid request outside the supported limits    */
+#define MOE_EHIP (-3)     /* a HIP runtime call failed                     */
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* moe_last_error(void);
+
+/* Library ABI version (major*10000 + minor*100 + patch). */
+int moe_version(void);
+
+/* Algorithm MOE_TOPK_AUTO resolves to for a row length N and top-K.
+ * Replaces _select_strategy (kernels/topk_softmax_tilelang.py:1056-1100),
+ * with the thresholds of the reference README (README.md:120-122):
+ * N<=64 -> bitonic, 65<=N<=512 -> selection, N>512 -> radix. */
+int moe_topk_select_algo(int64_t N, int64_t K);
+
+/* Workspace bytes moe_topk_softmax needs for this shape and algorithm
+ * (0 for bitonic and selection). */
+size_t moe_topk_softmax_workspace_size(int64_t M, int64_t N, int64_t K, int algo);
+
+/* Fused TopK + softmax over the last dimension of a row-major [M, N] matrix.
+ *
+ * Replaces topk_softmax_best (kernels/topk_softmax_tilelang.py:1103-1135)
+ * and, per branch, topk_softmax_bitonic (:895-921), topk_softmax_selection
+ * (:983-1001) and topk_radix_tilelang + torch gather/softmax (:205-235,
+ * :1128-1131).  Semantics are those of the reference's PyTorch baseline
+ * topk_softmax_fused (kernels/topk_softmax_baseline.py:39-66):
+ *     v, i = topk(logits, K, dim=-1)            (sorted, descending)
+ *     scores = softmax(v, dim=-1, dtype=fp32)
+ * with one deterministic tie rule: equal values are ordered by ascending
+ * index; -0.0 equals +0.0; NaN ranks above +inf.
+ *
+ *   logits        [M, N] rows, row stride `ld` elements (ld >= N),
+ *                 dtype MOE_F32, MOE_BF16 or MOE_F16
+ *   scores        [M, K] fp32, contiguous; may be NULL (indices only, the
+ *                 reference's topk_radix_tilelang)
+ *   indices       [M, K] contiguous, idx_dtype MOE_I32 or MOE_I64
+ *   algo          enum moe_topk_algo
+ *   workspace     >= moe_topk_softmax_workspace_size(M, N, K, algo) bytes
+ *                 (may be NULL when that size is 0)
+ */
+int moe_topk_softmax(const void* logits, int logits_dtype, int64_t M, int64_t N,
+                     int64_t ld, int64_t K, float* scores, void* indices,
+                     int idx_dtype, int algo, void* workspace, size_t ws_bytes,
+                     void* stream);
+
+/* Workspace bytes moe_route_sort needs for R routed rows over E experts. */
+size_t moe_route_sort_workspace_size(int64_t R, int64_t E);
+
+/* Workspace bytes moe_grouped_gemm needs for R = T*topk routed rows over E
+ * experts with output width I. */
+size_t moe_grouped_gemm_workspace_size(int64_t T, int64_t topk, int64_t E, int64_t I);
+
+/* Device-side counting sort of routed rows by expert: the segment-offset
+ * pass that replaces the host-side argsort / bincount().tolist() / Python
+ * offset loops of grouped_gemm_tilelang_v2 and grouped_gemm_pytorch
+ * (kernels/grouped_gemm_tilelang.py:562-569, :700-729).
+ *
+ *   expert_ids  [R] expert id per row, idx_dtype MOE_I32 or MOE_I64
+ *   counts      [E]   rows per expert                       (int32, out)
+ *   offsets     [E+1] exclusive prefix sum of counts; offsets[E] = number
+ *               of rows whose id lies in [0, E)              (int32, out)
+ *   sorted_rows [R]   row numbers grouped by expert: rows of expert e are
+ *               sorted_rows[offsets[e] .. offsets[e+1]), in ascending row
+ *               order; rows with an id outside [0, E) follow in ascending
+ *               order at sorted_rows[offsets[E] .. R)         (int32, out)
+ *   workspace   >= moe_route_sort_workspace_size(R, E) bytes
+ *   Limits: R < 2^31, 1 <= E <= 4096.
+ */
+int moe_route_sort(const void* expert_ids, int idx_dtype, int64_t R, int64_t E,
+                   int32_t* counts, int32_t* offsets, int32_t* sorted_rows,
+                   void* workspace, size_t ws_bytes, void* stream);
+
+/* Expert grouped GEMM: Y[r, :] = X[r / topk, :] @ W[expert_ids[r], :, :]^T
+ *
+ * Replaces grouped_gemm_best (kernels/grouped_gemm_tilelang.py:859-890) and
+ * both of its branches, grouped_gemm_tilelang_v2 (:682-766) and the E>64
+ * per-expert torch.mm loop grouped_gemm_pytorch (:542-601).  Semantics are
+ * those of grouped_gemm_loop (kernels/grouped_gemm_baseline.py:14-57):
+ * fp32 accumulation, output in the input dtype, rows whose expert id lies
+ * outside [0, E) are zero.  topk == 1 is exactly the reference's 1-D
+ * signature (X [R, H], expert_ids [R]); topk > 1 gathers token r / topk of
+ * X [T, H] for routed row r of expert_ids [T, topk] (the identity
+ * grouped_gemm(X.repeat_interleave(topk, 0), W, ids.flatten())).
+ *
+ *   X           [T, H] row-major, dtype MOE_BF16 or MOE_F16, 16-byte aligned
+ *   W           [E, I, H] row-major, same dtype, 16-byte aligned
+ *   expert_ids  [T*topk], idx_dtype MOE_I32 or MOE_I64
+ *   Y           [T*topk, I] row-major, same dtype as X
+ *   H must be a multiple of 8.
+ */
+int moe_grouped_gemm(const void* X, const void* W, const void* expert_ids,
+                     int dtype, int idx_dtype, int64_t T, int64_t topk, int64_t H,
+                     int64_t I, int64_t E, void* Y, void* workspace,
+                     size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_HIP_H */

@@ -1,0 +1,37 @@
+"""Drop-in package API for the MoE routed-expert hot path.
+
+Mirrors the hot-path names of the reference's kernels/__init__.py
+(:11-22 TopK+softmax, :31-35 grouped GEMM): ``topk_softmax`` and
+``grouped_gemm`` are the recommended entry points, the other names are the
+per-algorithm variants the reference also exports.  Every function runs a
+hand-written gfx950 HIP kernel from libmoe_hip.so.
+"""
+from .topk_softmax import (
+    select_strategy,
+    topk_radix,
+    topk_radix_tilelang,
+    topk_softmax,
+    topk_softmax_best,
+    topk_softmax_bitonic,
+    topk_softmax_int64,
+    topk_softmax_radix,
+    topk_softmax_selection,
+    topk_softmax_sonic,
+)
+from .grouped_gemm import grouped_gemm, grouped_gemm_best, route_sort
+
+__all__ = [
+    "topk_softmax",
+    "topk_softmax_best",
+    "topk_softmax_bitonic",
+    "topk_softmax_selection",
+    "topk_softmax_sonic",
+    "topk_softmax_radix",
+    "topk_softmax_int64",
+    "topk_radix",
+    "topk_radix_tilelang",
+    "select_strategy",
+    "grouped_gemm",
+    "grouped_gemm_best",
+    "route_sort",
+]

@@ -1,0 +1,120 @@
+"""Expert grouped GEMM (drop-in for the reference's grouped_gemm).
+
+Reference interface (kernels/grouped_gemm_tilelang.py):
+  grouped_gemm_best(X [R,H], W [E,I,H], expert_indices [R]) -> Y [R,I]   :859-890
+    H*I <= 2048*1024 -> grouped_gemm_tilelang_v2 (:682-766)
+    otherwise        -> grouped_gemm_pytorch, a per-expert torch.mm loop (:542-601)
+
+Here every shape runs one device pipeline from libmoe_hip.so: a routing sort
+(per-expert counts, segment offsets, stable row permutation, M-tile table),
+then one bf16/fp16 MFMA kernel whose A-tile load gathers X rows through the
+permutation and whose epilogue stores rows back in routed order.  There is no
+host synchronisation, no per-routing recompilation and no per-call weight
+transpose.  Semantics are those of grouped_gemm_loop
+(kernels/grouped_gemm_baseline.py:14-57): fp32 accumulation, output in X's
+dtype, rows whose expert id lies outside [0, E) are zero.
+"""
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+
+from .. import _lib
+
+_DTYPES = {torch.bfloat16: _lib.MOE_BF16, torch.float16: _lib.MOE_F16}
+_IDX = {torch.int32: _lib.MOE_I32, torch.int64: _lib.MOE_I64}
+
+
+def _stream(dev: torch.device) -> int:
+    with torch.cuda.device(dev):
+        return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _check_ids(expert_indices: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    if not isinstance(expert_indices, torch.Tensor):
+        raise TypeError("expert_indices must be a torch.Tensor")
+    if expert_indices.dtype not in _IDX:
+        raise ValueError(f"expert_indices must be int32 or int64, got {expert_indices.dtype}")
+    if expert_indices.device != dev:
+        raise ValueError("expert_indices must be on the same device as X")
+    return expert_indices.contiguous()
+
+
+def grouped_gemm(X: torch.Tensor, W: torch.Tensor, expert_indices: torch.Tensor) -> torch.Tensor:
+    """``Y[r] = X[r] @ W[expert_indices[r]].T`` for every routed row r.
+
+    X: [R, H] bf16/fp16; W: [E, I, H] same dtype; expert_indices: [R] int32/int64.
+    Also accepts expert_indices of shape [T, topk] with X [T, H]: routed row
+    r = t*topk + j then reads token t, which equals the reference applied to
+    ``X.repeat_interleave(topk, 0)`` and ``expert_indices.flatten()`` without
+    materialising the repeated X.  Returns Y [R, I] (R = T*topk) in X's dtype.
+    """
+    if not isinstance(X, torch.Tensor) or not isinstance(W, torch.Tensor):
+        raise TypeError("X and W must be torch.Tensors")
+    if X.dim() != 2 or W.dim() != 3:
+        raise ValueError(f"expected X [R,H] and W [E,I,H], got {tuple(X.shape)} and {tuple(W.shape)}")
+    if X.device.type != "cuda" or W.device != X.device:
+        raise ValueError("grouped_gemm runs on the GPU only: X and W must be cuda (HIP) tensors "
+                         "on one device")
+    if X.dtype not in _DTYPES or W.dtype != X.dtype:
+        raise ValueError(f"X and W must both be bfloat16 or both float16, got {X.dtype} and {W.dtype}")
+    T, H = X.shape
+    E, I, H2 = W.shape
+    if H2 != H:
+        raise ValueError(f"hidden size mismatch: X has H={H}, W has H={H2}")
+    ids = _check_ids(expert_indices, X.device)
+    if ids.dim() == 1:
+        topk = 1
+        if ids.shape[0] != T:
+            raise ValueError(f"expert_indices has {ids.shape[0]} rows, X has {T}")
+    elif ids.dim() == 2:
+        topk = ids.shape[1]
+        if ids.shape[0] != T:
+            raise ValueError(f"expert_indices [T, topk] has T={ids.shape[0]}, X has {T}")
+    else:
+        raise ValueError("expert_indices must be [R] or [T, topk]")
+    R = T * topk
+    X = X.contiguous()
+    W = W.contiguous()
+    Y = torch.empty((R, I), dtype=X.dtype, device=X.device)
+    if R == 0 or topk == 0:
+        return Y
+    L = _lib.lib()
+    ws_bytes = L.moe_grouped_gemm_workspace_size(T, topk, E, I)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=X.device)
+    _lib.check(L.moe_grouped_gemm(X.data_ptr(), W.data_ptr(), ids.data_ptr(), _DTYPES[X.dtype],
+                                  _IDX[ids.dtype], T, topk, H, I, E, Y.data_ptr(), ws.data_ptr(),
+                                  ws_bytes, _stream(X.device)))
+    return Y
+
+
+grouped_gemm_best = grouped_gemm
+
+
+def route_sort(expert_indices: torch.Tensor, num_experts: int
+               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Device counting sort of routed rows by expert.
+
+    Returns ``(counts int32 [E], offsets int32 [E+1], sorted_rows int32 [R])``:
+    rows of expert e are ``sorted_rows[offsets[e]:offsets[e+1]]`` in ascending
+    order, rows with an id outside [0, E) follow from ``offsets[E]``.  This is
+    the device replacement of the reference's argsort + bincount().tolist() +
+    Python offset loops (kernels/grouped_gemm_tilelang.py:700-729).
+    """
+    if not isinstance(expert_indices, torch.Tensor) or expert_indices.device.type != "cuda":
+        raise ValueError("route_sort runs on the GPU only: expert_indices must be a cuda tensor")
+    ids = _check_ids(expert_indices, expert_indices.device).reshape(-1)
+    E = int(num_experts)
+    R = ids.numel()
+    dev = ids.device
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    sorted_rows = torch.empty(R, dtype=torch.int32, device=dev)
+    L = _lib.lib()
+    ws_bytes = L.moe_route_sort_workspace_size(R, E)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    _lib.check(L.moe_route_sort(ids.data_ptr(), _IDX[ids.dtype], R, E, counts.data_ptr(),
+                                offsets.data_ptr(), sorted_rows.data_ptr(), ws.data_ptr(), ws_bytes,
+                                _stream(dev)))
+    return counts, offsets, sorted_rows

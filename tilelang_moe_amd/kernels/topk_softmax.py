@@ -1,0 +1,138 @@
+"""Fused TopK + softmax router (drop-in for the reference's topk_softmax).
+
+Reference interface (kernels/topk_softmax_tilelang.py):
+  topk_softmax_best(logits, k) -> (scores fp32 [M,k], indices int32 [M,k])   :1103-1135
+  topk_softmax_bitonic(logits, k)                                            :895-921
+  topk_softmax_selection(logits, k)   (alias topk_softmax_sonic)             :983-1004
+  topk_radix_tilelang(logits, topk) -> indices int32 [M,topk]                :205-235
+  _select_strategy(num_experts, k)                                           :1056-1100
+
+Semantics follow the reference's PyTorch baseline topk_softmax_fused
+(kernels/topk_softmax_baseline.py:39-66): the k largest logits of each row in
+descending order, softmax over those k values in fp32.  Ties are broken by
+ascending column index (torch.sort(stable=True) order); -0.0 == +0.0; NaN
+ranks above +inf.  Every call runs a hand-written gfx950 kernel from
+libmoe_hip.so on the tensor's device and current stream; CPU tensors are
+rejected.
+"""
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+
+from .. import _lib
+
+_LOGIT_DTYPES = {torch.float32: _lib.MOE_F32, torch.bfloat16: _lib.MOE_BF16,
+                 torch.float16: _lib.MOE_F16}
+_IDX_DTYPES = {torch.int32: _lib.MOE_I32, torch.int64: _lib.MOE_I64}
+_ALGOS = {"auto": _lib.MOE_TOPK_AUTO, "bitonic": _lib.MOE_TOPK_BITONIC,
+          "selection": _lib.MOE_TOPK_SELECTION, "radix": _lib.MOE_TOPK_RADIX}
+_ALGO_NAMES = {v: k for k, v in _ALGOS.items()}
+
+
+def select_strategy(num_experts: int, k: int) -> str:
+    """Name of the algorithm ``topk_softmax`` uses for rows of ``num_experts``.
+
+    Thresholds of the reference README (README.md:120-122): N<=64 bitonic,
+    65..512 selection, N>512 radix.  (The reference code's _select_strategy,
+    kernels/topk_softmax_tilelang.py:1056-1100, agrees on every BASELINE shape.)
+    """
+    return _ALGO_NAMES[_lib.lib().moe_topk_select_algo(int(num_experts), int(k))]
+
+
+def _check_logits(logits: torch.Tensor, k) -> Tuple[torch.Tensor, int]:
+    if not isinstance(logits, torch.Tensor):
+        raise TypeError("logits must be a torch.Tensor")
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be 2-D [num_tokens, num_experts], got shape {tuple(logits.shape)}")
+    if logits.dtype not in _LOGIT_DTYPES:
+        raise ValueError(f"logits dtype must be float32, bfloat16 or float16, got {logits.dtype}")
+    if logits.device.type != "cuda":
+        raise ValueError("topk_softmax runs on the GPU only: logits must be a cuda (HIP) tensor")
+    if isinstance(k, torch.Tensor):
+        k = int(k.item())
+    k = int(k)
+    n = logits.shape[1]
+    if not 1 <= k <= n:
+        raise ValueError(f"k must satisfy 1 <= k <= num_experts={n}, got {k}")
+    if logits.stride(1) != 1 or logits.stride(0) < n:
+        logits = logits.contiguous()
+    return logits, k
+
+
+def _run(logits: torch.Tensor, k: int, algo: int, with_scores: bool,
+         index_dtype: torch.dtype = torch.int32):
+    logits, k = _check_logits(logits, k)
+    m, n = logits.shape
+    dev = logits.device
+    indices = torch.empty((m, k), dtype=index_dtype, device=dev)
+    scores = torch.empty((m, k), dtype=torch.float32, device=dev) if with_scores else None
+    if m == 0:
+        return scores, indices
+    L = _lib.lib()
+    ws_bytes = L.moe_topk_softmax_workspace_size(m, n, k, algo)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+    _lib.check(L.moe_topk_softmax(
+        logits.data_ptr(), _LOGIT_DTYPES[logits.dtype], m, n, logits.stride(0), k,
+        scores.data_ptr() if with_scores else None, indices.data_ptr(), _IDX_DTYPES[index_dtype],
+        algo, ws.data_ptr() if ws is not None else None, ws_bytes, stream))
+    return scores, indices
+
+
+def topk_softmax(logits: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Auto-selected fused TopK+softmax: ``(scores fp32 [M,k], indices int32 [M,k])``.
+
+    Drop-in for topk_softmax / topk_softmax_best (kernels/__init__.py:21,
+    kernels/topk_softmax_tilelang.py:1103-1135).  Unlike the reference's radix
+    branch, the radix path also returns indices sorted by descending score.
+    """
+    return _run(logits, k, _lib.MOE_TOPK_AUTO, True)
+
+
+topk_softmax_best = topk_softmax
+
+
+def topk_softmax_bitonic(logits: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Wave64 bitonic-network TopK+softmax, num_experts <= 64
+    (reference: topk_softmax_bitonic, kernels/topk_softmax_tilelang.py:895-921,
+    which allows up to 1024 and raises ValueError beyond)."""
+    return _run(logits, k, _lib.MOE_TOPK_BITONIC, True)
+
+
+def topk_softmax_selection(logits: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Selection TopK+softmax (K rounds of wave argmax), num_experts <= 1024
+    (reference: topk_softmax_selection, kernels/topk_softmax_tilelang.py:983-1001)."""
+    return _run(logits, k, _lib.MOE_TOPK_SELECTION, True)
+
+
+topk_softmax_sonic = topk_softmax_selection
+
+
+def topk_softmax_radix(logits: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Radix-select TopK with the softmax fused in the same kernel (the
+    reference's radix branch of topk_softmax_best, :1126-1131, runs radix,
+    then torch.gather and torch.softmax)."""
+    return _run(logits, k, _lib.MOE_TOPK_RADIX, True)
+
+
+def topk_radix(logits: torch.Tensor, topk: int = 6) -> torch.Tensor:
+    """Indices-only radix TopK, int32 [M, topk], sorted by descending value.
+
+    Drop-in for topk_radix_tilelang (kernels/topk_softmax_tilelang.py:205-235),
+    which returns the same index set in unspecified order.
+    """
+    return _run(logits, topk, _lib.MOE_TOPK_RADIX, False)[1]
+
+
+# Name used by the reference's package API (kernels/__init__.py:11).
+topk_radix_tilelang = topk_radix
+
+
+def topk_softmax_int64(logits: torch.Tensor, k: int, algo: str = "auto"
+                       ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Same as ``topk_softmax`` with int64 indices (the dtype torch.topk and the
+    reference baseline return); ``algo`` forces one of auto/bitonic/selection/radix."""
+    return _run(logits, k, _ALGOS[algo], True, torch.int64)
