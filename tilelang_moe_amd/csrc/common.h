@@ -27,6 +27,19 @@ int check_launch(const char* what);
 
 constexpr int kWave = 64;
 
+// Phase timestamps for kernel tuning builds (-DMOE_PHASE_TIMING): thread 0
+// of each workgroup records the wall clock into moe_phase[block][slot].
+#ifdef MOE_PHASE_TIMING
+#define MOE_PHASE(slot)                                                        \
+  do {                                                                         \
+    if (threadIdx.x == 0) moe_phase[blockIdx.x * 16 + (slot)] = wall_clock64(); \
+  } while (0)
+#else
+#define MOE_PHASE(slot) \
+  do {                  \
+  } while (0)
+#endif
+
 // ---------------------------------------------------------------------------
 // Order-preserving 32-bit keys.  key(a) > key(b)  <=>  a > b, with -0.0 and
 // +0.0 mapped to one key and every NaN mapped to the largest key (torch.topk
@@ -37,6 +50,15 @@ __host__ __device__ inline uint32_t key_of_bits(uint32_t u) {
   if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0xFFFFFFFFu;  // NaN
   if (u == 0x80000000u) u = 0u;                              // -0 -> +0
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Plain sign-flip key (3 ALU ops): equals key_of_bits except for NaN and
+// -0.0, which callers detect and re-key.
+__host__ __device__ inline uint32_t key_fast(uint32_t u) {
+  return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+__host__ __device__ inline uint32_t bits_of_fast_key(uint32_t k) {
+  return (k & 0x80000000u) ? (k ^ 0x80000000u) : ~k;
 }
 
 __host__ __device__ inline float value_of_key(uint32_t k) {
@@ -74,24 +96,138 @@ template <> struct Elem<Half16> {
 
 // ---------------------------------------------------------------------------
 // Wave64 cross-lane helpers.
+// xor_lanes<M> returns x from lane (lane ^ M) without going through the LDS
+// crossbar: DPP quad permutes for M = 1, 2, DPP row shifts for 4, a DPP row
+// rotate for 8 and the gfx950 v_permlane16/32_swap for 16 and 32.  Scans and
+// reductions are DPP row shifts / mirrors plus row broadcasts or readlanes.
 // ---------------------------------------------------------------------------
 __device__ inline uint32_t lane_id() { return __lane_id(); }
 
-__device__ inline uint64_t shfl_xor_u64(uint64_t v, int mask) {
-  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-  lo = __shfl_xor(lo, mask, kWave);
-  hi = __shfl_xor(hi, mask, kWave);
-  return ((uint64_t)hi << 32) | lo;
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ inline uint32_t dpp(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppRowShl4 = 0x104;     // lane n <- n+4 (within a 16-lane row)
+constexpr int kDppRowShr1 = 0x111;     // lane n <- n-1
+constexpr int kDppRowShr2 = 0x112;
+constexpr int kDppRowShr4 = 0x114;
+constexpr int kDppRowShr8 = 0x118;
+constexpr int kDppRowRor8 = 0x128;     // lane n <- (n+8) mod 16 = n^8
+constexpr int kDppRowMirror = 0x140;   // lane n <- 15-n
+constexpr int kDppRowHalfMirror = 0x141;  // lane n <- 7-n (within 8)
+constexpr int kDppRowBcast15 = 0x142;  // row r+1 <- lane 15 of row r
+constexpr int kDppRowBcast31 = 0x143;  // rows 2,3 <- lane 31
+
+template <int M>
+__device__ inline uint32_t xor_lanes(uint32_t x) {
+  if constexpr (M == 1) {
+    return dpp<kDppQuadXor1>(x, x);
+  } else if constexpr (M == 2) {
+    return dpp<kDppQuadXor2>(x, x);
+  } else if constexpr (M == 4) {
+    const uint32_t up = dpp<kDppRowShl4>(x, x), dn = dpp<kDppRowShr4>(x, x);
+    return (__lane_id() & 4) ? dn : up;
+  } else if constexpr (M == 8) {
+    return dpp<kDppRowRor8>(x, x);
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return ((__lane_id() >> 4) & 1) ? r[0] : r[1];
+  } else {
+    static_assert(M == 32, "xor_lanes: M must be a power of two below 64");
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (__lane_id() < 32) ? r[1] : r[0];
+  }
 }
 
-__device__ inline uint64_t shfl_u64(uint64_t v, int src) {
-  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-  lo = __shfl(lo, src, kWave);
-  hi = __shfl(hi, src, kWave);
+template <int M>
+__device__ inline uint64_t xor_lanes_u64(uint64_t v) {
+  const uint32_t lo = xor_lanes<M>((uint32_t)v), hi = xor_lanes<M>((uint32_t)(v >> 32));
   return ((uint64_t)hi << 32) | lo;
+}
+template <int M>
+__device__ inline float xor_lanes_f32(float v) {
+  return __uint_as_float(xor_lanes<M>(__float_as_uint(v)));
+}
+
+// Runtime-mask variant (M a power of two < 64) for loops the compiler unrolls.
+__device__ inline uint64_t xor_lanes_u64(uint64_t v, int m) {
+  switch (m) {
+    case 1: return xor_lanes_u64<1>(v);
+    case 2: return xor_lanes_u64<2>(v);
+    case 4: return xor_lanes_u64<4>(v);
+    case 8: return xor_lanes_u64<8>(v);
+    case 16: return xor_lanes_u64<16>(v);
+    default: return xor_lanes_u64<32>(v);
+  }
+}
+__device__ inline float xor_lanes_f32(float v, int m) {
+  const uint32_t u = __float_as_uint(v);
+  uint32_t r;
+  switch (m) {
+    case 1: r = xor_lanes<1>(u); break;
+    case 2: r = xor_lanes<2>(u); break;
+    case 4: r = xor_lanes<4>(u); break;
+    case 8: r = xor_lanes<8>(u); break;
+    case 16: r = xor_lanes<16>(u); break;
+    default: r = xor_lanes<32>(u); break;
+  }
+  return __uint_as_float(r);
+}
+
+// Inclusive prefix sum over the 64 lanes.
+__device__ inline uint32_t wave_incl_scan(uint32_t x) {
+  x += dpp<kDppRowShr1>(0u, x);
+  x += dpp<kDppRowShr2>(0u, x);
+  x += dpp<kDppRowShr4>(0u, x);
+  x += dpp<kDppRowShr8>(0u, x);
+  x += dpp<kDppRowBcast15, 0xA>(0u, x);
+  x += dpp<kDppRowBcast31, 0xC>(0u, x);
+  return x;
+}
+
+// All-lane reductions.
+__device__ inline uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, dpp<kDppQuadXor1>(x, x));
+  x = max(x, dpp<kDppQuadXor2>(x, x));
+  x = max(x, dpp<kDppRowHalfMirror>(x, x));
+  x = max(x, dpp<kDppRowMirror>(x, x));
+  const uint32_t a = __builtin_amdgcn_readlane(x, 0), b = __builtin_amdgcn_readlane(x, 16);
+  const uint32_t c = __builtin_amdgcn_readlane(x, 32), d = __builtin_amdgcn_readlane(x, 48);
+  return max(max(a, b), max(c, d));
+}
+
+__device__ inline float wave_sum_f32(float v) {
+  uint32_t x = __float_as_uint(v);
+  x = __float_as_uint(__uint_as_float(x) + __uint_as_float(dpp<kDppQuadXor1>(x, x)));
+  x = __float_as_uint(__uint_as_float(x) + __uint_as_float(dpp<kDppQuadXor2>(x, x)));
+  x = __float_as_uint(__uint_as_float(x) + __uint_as_float(dpp<kDppRowHalfMirror>(x, x)));
+  x = __float_as_uint(__uint_as_float(x) + __uint_as_float(dpp<kDppRowMirror>(x, x)));
+  const float a = __uint_as_float(__builtin_amdgcn_readlane(x, 0));
+  const float b = __uint_as_float(__builtin_amdgcn_readlane(x, 16));
+  const float c = __uint_as_float(__builtin_amdgcn_readlane(x, 32));
+  const float d = __uint_as_float(__builtin_amdgcn_readlane(x, 48));
+  return (a + b) + (c + d);
 }
 
 __device__ inline uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 __device__ inline uint64_t umin64(uint64_t a, uint64_t b) { return a < b ? a : b; }
+
+__device__ inline uint64_t readlane_u64(uint64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ inline uint64_t wave_max_u64(uint64_t x) {
+  x = umax64(x, xor_lanes_u64<1>(x));
+  x = umax64(x, xor_lanes_u64<2>(x));
+  x = umax64(x, xor_lanes_u64<4>(x));
+  x = umax64(x, xor_lanes_u64<8>(x));
+  const uint64_t a = readlane_u64(x, 0), b = readlane_u64(x, 16);
+  const uint64_t c = readlane_u64(x, 32), d = readlane_u64(x, 48);
+  return umax64(umax64(a, b), umax64(c, d));
+}
 
 }  // namespace moe

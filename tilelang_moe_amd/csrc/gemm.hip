@@ -59,12 +59,7 @@ __device__ inline int32_t block_excl_scan(int32_t v, int32_t* wsum) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
-  int32_t incl = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int32_t t = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += t;
-  }
+  const int32_t incl = (int32_t)wave_incl_scan((uint32_t)v);
   if (lane == kWave - 1) wsum[wave] = incl;
   __syncthreads();
   int32_t base = 0;
@@ -73,29 +68,50 @@ __device__ inline int32_t block_excl_scan(int32_t v, int32_t* wsum) {
   return base + incl - v;
 }
 
-// Single workgroup.  In: blockcnt ([E+1][nb] counts).  Out: blockcnt turned
-// into exclusive offsets, counts[E], offsets[E+1] and, when bm > 0, the GEMM
-// M-tile table (tile_expert, tile_mstart, meta[0] = number of tiles).
+// Single workgroup.  In: blockcnt ([E+1][nb] counts, nb <= 64).  Out:
+// blockcnt[e][b] = rows of expert e in chunks before b (one wave scans one
+// expert's nb counts with a single coalesced load), counts[E], offsets[E+1]
+// and, when bm > 0, the GEMM M-tile table (tile_expert, tile_mstart,
+// meta[0] = number of tiles).
 __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     int32_t* __restrict__ blockcnt, int64_t R, int E, int nb, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int bm, int32_t* __restrict__ tile_expert,
     int32_t* __restrict__ tile_mstart, int32_t* __restrict__ meta) {
-  __shared__ int32_t wsum[kScanThreads / kWave];
+  constexpr int NW = kScanThreads / kWave;
+  constexpr int UNROLL = 4;
+  __shared__ int32_t wsum[NW];
   __shared__ int32_t s_off[kMaxExperts + 2];
-  const int tid = threadIdx.x;
-  const int64_t L = (int64_t)(E + 1) * nb;
-  const int64_t per = (L + kScanThreads - 1) / kScanThreads;
-  const int64_t lo = std::min<int64_t>(L, tid * per), hi = std::min<int64_t>(L, lo + per);
-  int32_t sum = 0;
-  for (int64_t i = lo; i < hi; ++i) sum += blockcnt[i];
-  int32_t run = block_excl_scan(sum, wsum);
-  for (int64_t i = lo; i < hi; ++i) {
-    const int32_t c = blockcnt[i];
-    blockcnt[i] = run;
-    run += c;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  for (int e0 = wave * UNROLL; e0 <= E; e0 += NW * UNROLL) {
+    int32_t v[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+      v[u] = (e0 + u <= E && lane < nb) ? blockcnt[(int64_t)(e0 + u) * nb + lane] : 0;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int32_t incl = (int32_t)wave_incl_scan((uint32_t)v[u]);
+      if (e0 + u <= E) {
+        if (lane < nb) blockcnt[(int64_t)(e0 + u) * nb + lane] = incl - v[u];
+        if (lane == kWave - 1) s_off[e0 + u] = incl;  // expert total
+      }
+    }
   }
   __syncthreads();
-  for (int e = tid; e <= E; e += kScanThreads) s_off[e] = blockcnt[(int64_t)e * nb];
+  // Exclusive scan of the E+1 expert totals (contiguous runs per thread).
+  const int per = (E + 1 + kScanThreads - 1) / kScanThreads;
+  const int lo = std::min(E + 1, tid * per), hi = std::min(E + 1, lo + per);
+  int32_t tot[8], sum = 0;  // per <= 5 for E <= 4096
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    tot[q] = (lo + q < hi) ? s_off[lo + q] : 0;
+    sum += tot[q];
+  }
+  int32_t run = block_excl_scan(sum, wsum);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    if (lo + q < hi) s_off[lo + q] = run;
+    run += tot[q];
+  }
   if (tid == 0) s_off[E + 1] = (int32_t)R;
   __syncthreads();
   for (int e = tid; e <= E; e += kScanThreads) {
@@ -123,14 +139,15 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
 template <typename IdxT>
 __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
     const IdxT* __restrict__ ids, int64_t R, int E, int chunk, int nb,
-    const int32_t* __restrict__ blockoff, int32_t* __restrict__ sorted_rows) {
+    const int32_t* __restrict__ blockoff, const int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_rows) {
   extern __shared__ int32_t sm[];  // base[E+1], wcnt[4][E+1]
   constexpr int NW = kRouteThreads / kWave;
   int32_t* base = sm;
   int32_t* wcnt = sm + (E + 1);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int nbits = 32 - __clz(E);  // bucket values lie in [0, E]
-  for (int e = tid; e <= E; e += kRouteThreads) base[e] = blockoff[(int64_t)e * nb + blockIdx.x];
+  for (int e = tid; e <= E; e += kRouteThreads) base[e] = offsets[e] + blockoff[(int64_t)e * nb + blockIdx.x];
   const int64_t lo = (int64_t)blockIdx.x * chunk;
   const int64_t hi = std::min<int64_t>(R, lo + chunk);
   const uint64_t lt_mask = (1ull << lane) - 1ull;
@@ -338,8 +355,10 @@ struct RoutePlan {
 };
 
 static RoutePlan route_plan(int64_t R) {
-  int64_t chunk = kRouteThreads;
-  while ((R + chunk - 1) / chunk > 1024 && chunk < (1 << 20)) chunk <<= 1;
+  // At most one wave's worth (64) of chunks, so the scan of an expert's
+  // per-chunk counts is a single wave-wide load.
+  const int64_t per_chunk = (R + kWave - 1) / kWave;
+  const int64_t chunk = std::max<int64_t>(kRouteThreads, (per_chunk + kRouteThreads - 1) / kRouteThreads * kRouteThreads);
   RoutePlan p;
   p.chunk = (int)chunk;
   p.nb = (int)std::max<int64_t>(1, (R + chunk - 1) / chunk);
@@ -392,7 +411,7 @@ static int launch_route(const IdxT* ids, int64_t R, int E, int32_t* blockcnt, in
     attr_set = true;
   }
   route_scatter_kernel<IdxT><<<p.nb, kRouteThreads, scat_lds, st>>>(ids, R, E, p.chunk, p.nb, blockcnt,
-                                                                     sorted_rows);
+                                                                     offsets, sorted_rows);
   return check_launch("route_scatter_kernel");
 }
 
