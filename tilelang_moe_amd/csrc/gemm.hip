@@ -7,8 +7,9 @@
 //                         segment offsets, then the M-tile table
 //   route_scatter_kernel  stable placement of each routed row into its
 //                         expert segment (wave ballots + per-wave counts)
-//   grouped_gemm_kernel   128x128x64 tiles, LDS double buffer, 2x2 waves of
-//                         64x64 built from v_mfma_f32_32x32x16_{bf16,f16};
+//   grouped_gemm_kernel   128x256 (or 64x128) tiles, 2x2 waves built from
+//                         v_mfma_f32_32x32x16_{bf16,f16}, a 3-stage LDS ring
+//                         filled by global_load_lds_dwordx4;
 //                         the X row gather (r / topk) is fused into the A
 //                         tile load and the un-permute into the epilogue store
 // This replaces the reference's host-side argsort, bincount().tolist()
@@ -184,7 +185,9 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
 // ---------------------------------------------------------------------------
 // MFMA grouped GEMM.
 // ---------------------------------------------------------------------------
-constexpr int kBM = 128, kBN = 128, kBK = 64, kGemmThreads = 256;
+constexpr int kMinBM = 64;  // smallest M tile of any configuration (workspace sizing)
+
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 template <typename T> struct MfmaOp;
 template <> struct MfmaOp<uint16_t> {  // bfloat16
@@ -212,139 +215,242 @@ template <> struct MfmaOp<Half16> {  // float16
   }
 };
 
-// LDS tile: rows of kBK = 64 elements = 8 chunks of 16 bytes; chunk c of row
-// r is stored at chunk position c ^ (r & 7) so that the 32 rows read by one
-// MFMA operand fetch spread over all banks.
-__device__ inline int lds_slot(int r, int c) { return r * 8 + (c ^ (r & 7)); }
+// Tile configurations.  A workgroup computes a BM x BN tile of one expert
+// with WM x WN waves, each owning FM x FN blocks of 32x32 (v_mfma 32x32x16);
+// K advances BK elements per pipeline stage and STAGES stages are in LDS.
+//
+// LDS layout of a stage: A rows then B rows, each row BK elements = CPR
+// chunks of 16 bytes.  Chunk c of row r sits at position
+//   c ^ ((r / (8 / CPR)) % CPR),
+// so the 8 lanes an LDS cycle serves in an MFMA operand fetch (8 consecutive
+// rows, one chunk each) hit 8 different 16-byte bank groups.
+//
+// Global -> LDS copies are gfx950 global_load_lds_dwordx4: every lane
+// fetches one 16-byte chunk straight into LDS and a wave instruction fills
+// 1 KB (64 / CPR rows), so copies use no VGPRs and STAGES-1 k-tiles stay in
+// flight.  A lane picks the global chunk that belongs in its LDS slot.
+template <int BM_, int BN_, int WM_, int WN_, int BK_, int STAGES_, int MINB_ = 1>
+struct GemmCfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, BK = BK_, STAGES = STAGES_;
+  static constexpr int MINB = MINB_;              // workgroups resident per CU
+  static constexpr int SUPER = 32 * MINB;         // workgroups per XCD (32 CUs each)
+  static constexpr int SN_MAX = 4;                // N tiles per super-tile
+  static constexpr int CPR = BK / 8;             // 16-byte chunks per row
+  static constexpr int RPI = kWave / CPR;        // rows per copy instruction
+  static constexpr int WAVES = WM * WN, THREADS = WAVES * kWave;
+  static constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
+  static constexpr int A_INS = BM / RPI / WAVES, B_INS = BN / RPI / WAVES;  // per thread per stage
+  static constexpr int STAGE_ELEMS = (BM + BN) * BK;
+  static constexpr size_t LDS_BYTES = (size_t)STAGES * STAGE_ELEMS * 2;
+  static_assert(CPR == 4 || CPR == 8, "BK must be 32 or 64");
+  static_assert(FM >= 1 && FN >= 1 && A_INS >= 1 && B_INS >= 1, "bad tile configuration");
+  static_assert(A_INS * WAVES * RPI == BM && B_INS * WAVES * RPI == BN, "rows must split evenly over waves");
+  static_assert(LDS_BYTES + BM * 4 <= 160 * 1024, "LDS budget");
+  static __device__ inline int slot(int r, int c) { return r * CPR + (c ^ ((r / (8 / CPR)) % CPR)); }
+};
+using CfgLarge = GemmCfg<128, 256, 2, 2, 32, 2, 2>;  // 4 waves of 64x128, 48 KB LDS, 2 per CU
+using CfgSmall = GemmCfg<64, 128, 2, 2, 64, 3>;   // 4 waves of 32x64,    72 KB LDS
 
-template <typename T>
-__global__ __launch_bounds__(kGemmThreads, 2) void grouped_gemm_kernel(
+template <typename T, typename Cfg, int MODE = 0>  // MODE: tuning builds only (1 = copies only, 2 = MFMA only)
+__global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
     const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, uint16_t* __restrict__ Y,
     int64_t H, int64_t I, int topk, int64_t R, int E, int ntn,
     const int32_t* __restrict__ sorted_rows, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_mstart,
     const int32_t* __restrict__ meta) {
-  __shared__ u32x4 As[2][kBM * kBK / 8];
-  __shared__ u32x4 Bs[2][kBN * kBK / 8];
-  __shared__ int32_t srow[kBM];
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, S = Cfg::STAGES, CPR = Cfg::CPR;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];  // [S][(BM+BN)*BK]
+  __shared__ int32_t srow[BM];
 
   const int tid = threadIdx.x;
-  // XCD-aware order: the hardware deals consecutive workgroups round-robin
-  // over the 8 XCDs, so give each XCD a contiguous range of the work list
-  // (neighbouring N tiles of one M tile share the gathered X rows in L2).
-  const int G = gridDim.x;  // multiple of 8
-  const int w = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
-  const int mt = w / ntn, nt = w % ntn;
-  const int n0 = nt * kBN;
-  const int n_tiles = meta[0];
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
 
-  if (mt >= n_tiles) {
-    // Spare tiles zero the rows whose expert id lies outside [0, E).
-    const int64_t z0 = (int64_t)offsets[E] + (int64_t)(mt - n_tiles) * kBM;
-    for (int i = tid; i < kBM * kBN; i += kGemmThreads) {
-      const int64_t p = z0 + i / kBN;
-      const int64_t col = n0 + i % kBN;
+  // Work list and its order.  The grid is persistent: gridDim.x = 8 * SUPER
+  // workgroups, SUPER per XCD (the hardware deals consecutive workgroups
+  // round-robin over the 8 XCDs, so workgroup b runs on XCD b % 8).  Work is
+  // cut into super-tiles of SUPER items, SM M tiles x SN N tiles; in round i
+  // XCD x processes super-tile 8i + x, one item per workgroup.  The SN N
+  // tiles of an M tile share its gathered X rows and the SM M tiles of one
+  // expert share its weight slices in that XCD's L2, at the same K position,
+  // so a hot expert's weights are read from HBM about ceil(M_e / (SM*BM))
+  // times instead of once per M tile.  The tiles that zero rows whose
+  // expert id lies outside [0, E) follow the super-tiles.
+  constexpr int SUPER = Cfg::SUPER;
+  const int SN = min(ntn, Cfg::SN_MAX);
+  const int SM = SUPER / SN;
+  const int NG = (ntn + SN - 1) / SN;
+  const int n_tiles = meta[0];
+  const int n_super_raw = (n_tiles + SM - 1) / SM * NG * SUPER;
+  const bool by_super_raw = n_super_raw / SUPER >= 16;
+  // Length of the tile part of the list: padded to whole super-tiles when
+  // ordered by super-tile, exact otherwise.
+  const int n_super_items = by_super_raw ? n_super_raw : n_tiles * ntn;
+  const int64_t n_bad = R - offsets[E];
+  const int n_zero = (int)((n_bad + BM - 1) / BM) * ntn;
+  const int total = n_super_items + n_zero;
+  // Too few super-tiles to occupy every XCD (small problems): give each XCD
+  // one contiguous eighth of the list instead, walked SUPER items at a time.
+  const bool by_super = by_super_raw;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int share = (total + 7) >> 3;
+  int w = by_super ? xcd * SUPER + slot : xcd * share + slot;
+  const int w_end = by_super ? total : min(total, (xcd + 1) * share);
+  const int step = by_super ? gridDim.x : SUPER;
+  for (; w < w_end; w += step) {
+  __syncthreads();  // the previous tile's LDS reads are done
+  if (w >= n_super_items) {
+    const int z = w - n_super_items;
+    const int64_t z0 = (int64_t)offsets[E] + (int64_t)(z / ntn) * BM;
+    const int n0z = (z % ntn) * BN;
+    for (int i = tid; i < BM * BN; i += Cfg::THREADS) {
+      const int64_t p = z0 + i / BN;
+      const int64_t col = n0z + i % BN;
       if (p < R && col < I) Y[(int64_t)sorted_rows[p] * I + col] = 0;
     }
-    return;
+    continue;
   }
+  int mt, nt;
+  if (by_super) {
+    const int sup = w / SUPER, within = w % SUPER;
+    mt = (sup / NG) * SM + within / SN;
+    nt = (sup % NG) * SN + within % SN;
+  } else {
+    mt = w / ntn;  // list order M-major
+    nt = w % ntn;
+  }
+  if (mt >= n_tiles || nt >= ntn) continue;
+  const int n0 = nt * BN;
 
   const int e = tile_expert[mt];
   const int m0 = tile_mstart[mt];
   const int mend = offsets[e + 1];
-  if (tid < kBM) srow[tid] = (m0 + tid < mend) ? sorted_rows[m0 + tid] : -1;
+  for (int r = tid; r < BM; r += Cfg::THREADS) srow[r] = (m0 + r < mend) ? sorted_rows[m0 + r] : -1;
   __syncthreads();
 
-  // Global -> LDS copy plan: thread owns chunk kc of rows tid/8 + 32q.
-  const int kc = tid & 7;
-  const uint16_t* a_ptr[4];
-  const uint16_t* b_ptr[4];
+  // Copy plan: instruction i of wave v covers tile rows RPI*(v*INS + i) ..;
+  // lane l fills slot l: row l / CPR, position l % CPR.
+  const int crow = lane / CPR;
+  const int cchunk = (lane % CPR) ^ ((crow / (8 / CPR)) % CPR);
+  const uint16_t* a_src[Cfg::A_INS];
+  const uint16_t* b_src[Cfg::B_INS];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = (tid >> 3) + 32 * q;
+  for (int i = 0; i < Cfg::A_INS; ++i) {
+    const int r = Cfg::RPI * (wave * Cfg::A_INS + i) + crow;
     const int sr = srow[r];
-    a_ptr[q] = sr >= 0 ? X + (int64_t)(sr / topk) * H + kc * 8 : nullptr;
-    const int64_t n = n0 + r;
-    b_ptr[q] = n < I ? W + ((int64_t)e * I + n) * H + kc * 8 : nullptr;
+    // Rows past the expert's segment read token 0; their results are never stored.
+    a_src[i] = X + (int64_t)(sr >= 0 ? sr / topk : 0) * H + cchunk * 8;
   }
-
-  const int nk = (int)((H + kBK - 1) / kBK);
-  u32x4 ra[4], rb[4];
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-  auto gload = [&](int kt) {
-    const int64_t k = (int64_t)kt * kBK;
-    const bool kin = k + kc * 8 < H;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      ra[q] = (a_ptr[q] && kin) ? *reinterpret_cast<const u32x4*>(a_ptr[q] + k) : zero;
-      rb[q] = (b_ptr[q] && kin) ? *reinterpret_cast<const u32x4*>(b_ptr[q] + k) : zero;
-    }
+  for (int i = 0; i < Cfg::B_INS; ++i) {
+    const int64_t n = n0 + Cfg::RPI * (wave * Cfg::B_INS + i) + crow;
+    b_src[i] = W + ((int64_t)e * I + (n < I ? n : 0)) * H + cchunk * 8;
+  }
+  const int nk = (int)((H + BK - 1) / BK);
+  const bool ktail = (H % BK) != 0;
+
+  auto issue = [&](int kt) {
+    if (kt >= nk || MODE == 2) return;
+    uint16_t* st = smem + (kt % S) * Cfg::STAGE_ELEMS;
+    const int64_t k = (int64_t)kt * BK;
+    // Chunks past H (last k-tile only) read the row start; they are zeroed
+    // in LDS before use.
+    const int64_t koff = (k + cchunk * 8 < H) ? k : -(int64_t)cchunk * 8;
+#pragma unroll
+    for (int i = 0; i < Cfg::A_INS; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + koff),
+                                       (lds_void_t*)(st + (wave * Cfg::A_INS + i) * 512), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < Cfg::B_INS; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(b_src[i] + koff),
+                                       (lds_void_t*)(st + BM * BK + (wave * Cfg::B_INS + i) * 512), 16, 0, 0);
   };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = (tid >> 3) + 32 * q;
-      As[buf][lds_slot(r, kc)] = ra[q];
-      Bs[buf][lds_slot(r, kc)] = rb[q];
-    }
-  };
 
-  const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
-  const int wm = wave >> 1, wn = wave & 1;
-  f32x16 acc[2][2];
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  // 32-row blocks of this wave that hold routed rows (wave-uniform): the
+  // MFMAs of the others are skipped, so a tile costs MFMA time in
+  // proportion to its rows, rounded up to 32.
+  const int mcount = min(BM, mend - m0);
+  const int fm_act = min(Cfg::FM, max(0, (mcount - wm * Cfg::FM * 32 + 31) / 32));
+  f32x16 acc[Cfg::FM][Cfg::FN];
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
+  for (int i = 0; i < Cfg::FM; ++i)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
+    for (int j = 0; j < Cfg::FN; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < S - 1; ++p) issue(p);
+
   for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) gload(kt + 1);
-    const int buf = kt & 1;
-#pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      const int c = 2 * s + (lane >> 5);
-      u32x4 a[2], b[2];
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) {
-        const int r = wm * 64 + mi * 32 + (lane & 31);
-        a[mi] = As[buf][lds_slot(r, c)];
-      }
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        const int r = wn * 64 + ni * 32 + (lane & 31);
-        b[ni] = Bs[buf][lds_slot(r, c)];
-      }
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = MfmaOp<T>::run(a[mi], b[ni], acc[mi][ni]);
+    // Wait for this thread's copies of k-tile kt (the younger tiles, up to
+    // S-2 of them, stay in flight), then make everyone's copies visible.
+    const int younger = min(S - 2, nk - 1 - kt) * (Cfg::A_INS + Cfg::B_INS);
+    switch (younger) {  // s_waitcnt needs an immediate; the counts are small
+#define MOE_VMWAIT(n) case n: __builtin_amdgcn_s_waitcnt(((n) & 0xF) | ((((n) >> 4) & 3) << 14) | 0x0F70); break;
+      MOE_VMWAIT(0) MOE_VMWAIT(4) MOE_VMWAIT(6) MOE_VMWAIT(8) MOE_VMWAIT(12) MOE_VMWAIT(16)
+      MOE_VMWAIT(18) MOE_VMWAIT(24) MOE_VMWAIT(30) MOE_VMWAIT(32) MOE_VMWAIT(36) MOE_VMWAIT(40)
+      MOE_VMWAIT(48) MOE_VMWAIT(54) MOE_VMWAIT(60)
+#undef MOE_VMWAIT
+      default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
     }
-    if (kt + 1 < nk) sstore((kt + 1) & 1);
-    __syncthreads();
+    // Plain s_barrier: __syncthreads() would also wait for the younger
+    // k-tiles still in flight (its release fence drains vmcnt).
+    __builtin_amdgcn_s_barrier();
+    // All waves finished k-tile kt-1, so its slot may be refilled.
+    issue(kt + S - 1);
+    const uint16_t* st = smem + (kt % S) * Cfg::STAGE_ELEMS;
+    if (ktail && kt == nk - 1) {
+      // Zero the chunks past H of the last k-tile in both operands.
+      uint16_t* sw = const_cast<uint16_t*>(st);
+      const int64_t k = (int64_t)kt * BK;
+      for (int q = tid; q < (BM + BN) * CPR; q += Cfg::THREADS) {
+        const int r = q / CPR, pos = q % CPR, c = pos ^ ((r / (8 / CPR)) % CPR);
+        if (k + c * 8 >= H) *reinterpret_cast<u32x4*>(sw + q * 8) = u32x4{0u, 0u, 0u, 0u};
+      }
+      __syncthreads();
+    }
+    const u32x4* As = reinterpret_cast<const u32x4*>(st);
+    const u32x4* Bs = reinterpret_cast<const u32x4*>(st + BM * BK);
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int c = 2 * s + (lane >> 5);
+      u32x4 a[Cfg::FM], b[Cfg::FN];
+#pragma unroll
+      for (int i = 0; i < Cfg::FM; ++i)
+        if (i < fm_act) a[i] = As[Cfg::slot(wm * Cfg::FM * 32 + i * 32 + (lane & 31), c)];
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j) b[j] = Bs[Cfg::slot(wn * Cfg::FN * 32 + j * 32 + (lane & 31), c)];
+      if (MODE == 1) {
+        acc[0][0][0] += __uint_as_float(a[0][0] ^ b[0][0]);
+        continue;
+      }
+#pragma unroll
+      for (int i = 0; i < Cfg::FM; ++i)
+        if (i < fm_act)
+#pragma unroll
+          for (int j = 0; j < Cfg::FN; ++j) acc[i][j] = MfmaOp<T>::run(a[i], b[j], acc[i][j]);
+    }
   }
 
   // Epilogue: accumulator v of lane l holds row 8*(v/4) + 4*(l/32) + v%4,
-  // column l%32 of its 32x32 block.  Rows are scattered back to their
-  // original routed-row position.
+  // column l%32 of its 32x32 block.  Rows go back to their routed position.
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
+  for (int i = 0; i < Cfg::FM; ++i) {
+    if (i >= fm_act) continue;
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const int64_t col = n0 + wn * 64 + ni * 32 + (lane & 31);
+    for (int j = 0; j < Cfg::FN; ++j) {
+      const int64_t col = n0 + (wn * Cfg::FN + j) * 32 + (lane & 31);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int i = (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        const int sr = srow[wm * 64 + mi * 32 + i];
-        if (sr >= 0 && col < I) Y[(int64_t)sr * I + col] = MfmaOp<T>::cvt(acc[mi][ni][v]);
+        const int r = (wm * Cfg::FM + i) * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        const int sr = srow[r];
+        if (sr >= 0 && col < I) Y[(int64_t)sr * I + col] = MfmaOp<T>::cvt(acc[i][j][v]);
       }
     }
   }
+  }  // tile loop
 }
 
 // ---------------------------------------------------------------------------
@@ -378,7 +484,7 @@ struct GemmLayout {
 
 static GemmLayout gemm_layout(int64_t R, int64_t E) {
   GemmLayout g;
-  g.mt_ub = (R + kBM - 1) / kBM + E + 1;
+  g.mt_ub = (R + kMinBM - 1) / kMinBM + E + 1;
   size_t o = 0;
   g.blockcnt = o; o += route_scratch_bytes(R, E);
   g.counts = o; o += align_up(E * sizeof(int32_t));
@@ -413,6 +519,22 @@ static int launch_route(const IdxT* ids, int64_t R, int E, int32_t* blockcnt, in
   route_scatter_kernel<IdxT><<<p.nb, kRouteThreads, scat_lds, st>>>(ids, R, E, p.chunk, p.nb, blockcnt,
                                                                      offsets, sorted_rows);
   return check_launch("route_scatter_kernel");
+}
+
+template <typename T, typename Cfg, int MODE = 0>
+static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t H,
+                       int64_t I, int topk, int64_t R, int E, int ntn, const int32_t* sorted,
+                       const int32_t* offsets, const int32_t* t_exp, const int32_t* t_ms, const int32_t* meta) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    MOE_HIP_CHECK(hipFuncSetAttribute((const void*)grouped_gemm_kernel<T, Cfg, MODE>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cfg::LDS_BYTES));
+    attr_set = true;
+  }
+  // Persistent grid: SUPER workgroups per XCD (8 XCDs x 32 CUs x MINB).
+  grouped_gemm_kernel<T, Cfg, MODE><<<dim3(8 * Cfg::SUPER), Cfg::THREADS, Cfg::LDS_BYTES, st>>>(
+      x, w, y, H, I, topk, R, E, ntn, sorted, offsets, t_exp, t_ms, meta);
+  return MOE_OK;
 }
 
 }  // namespace moe
@@ -460,7 +582,7 @@ extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert
   if (E < 1 || E > kMaxExperts) return fail(MOE_EUNSUP, "grouped_gemm: need 1 <= E <= 4096");
   if (H % 8 != 0) return fail(MOE_EUNSUP, "grouped_gemm: H must be a multiple of 8");
   const int64_t R = T * topk;
-  if (R >= INT32_MAX || (R + kBM - 1) / kBM + E + 1 > (int64_t)INT32_MAX / ((I + kBN - 1) / kBN))
+  if (R >= INT32_MAX || (R + kMinBM - 1) / kMinBM + E + 1 > (int64_t)INT32_MAX / ((I + 63) / 64))
     return fail(MOE_EUNSUP, "grouped_gemm: problem too large");
   if (dtype != MOE_BF16 && dtype != MOE_F16)
     return fail(MOE_EINVAL, "grouped_gemm: X, W and Y must be bfloat16 or float16");
@@ -483,25 +605,29 @@ extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert
   int32_t* t_exp = reinterpret_cast<int32_t*>(ws + g.tile_expert);
   int32_t* t_ms = reinterpret_cast<int32_t*>(ws + g.tile_mstart);
   int32_t* meta = reinterpret_cast<int32_t*>(ws + g.meta);
+  // Large tiles when they still give every CU about two of them.
+  const bool large = ((R + CfgLarge::BM - 1) / CfgLarge::BM) * ((I + CfgLarge::BN - 1) / CfgLarge::BN) >= 512;
+  const int bm = large ? CfgLarge::BM : CfgSmall::BM;
+  const int bn = large ? CfgLarge::BN : CfgSmall::BN;
   int rc;
   if (idx_dtype == MOE_I64)
     rc = launch_route(static_cast<const int64_t*>(expert_ids), R, (int)E, blockcnt, counts, offsets, sorted,
-                      kBM, t_exp, t_ms, meta, st);
+                      bm, t_exp, t_ms, meta, st);
   else
     rc = launch_route(static_cast<const int32_t*>(expert_ids), R, (int)E, blockcnt, counts, offsets, sorted,
-                      kBM, t_exp, t_ms, meta, st);
+                      bm, t_exp, t_ms, meta, st);
   if (rc) return rc;
-  const int ntn = (int)((I + kBN - 1) / kBN);
-  int64_t grid = g.mt_ub * ntn;
-  grid = (grid + 7) / 8 * 8;
+  const int ntn = (int)((I + bn - 1) / bn);
   const uint16_t* x = static_cast<const uint16_t*>(X);
   const uint16_t* w = static_cast<const uint16_t*>(W);
   uint16_t* y = static_cast<uint16_t*>(Y);
-  if (dtype == MOE_BF16)
-    grouped_gemm_kernel<uint16_t><<<dim3((unsigned)grid), kGemmThreads, 0, st>>>(
-        x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
-  else
-    grouped_gemm_kernel<Half16><<<dim3((unsigned)grid), kGemmThreads, 0, st>>>(
-        x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
+  if (large) {
+    if (dtype == MOE_BF16) rc = launch_gemm<uint16_t, CfgLarge>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
+    else rc = launch_gemm<Half16, CfgLarge>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
+  } else {
+    if (dtype == MOE_BF16) rc = launch_gemm<uint16_t, CfgSmall>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
+    else rc = launch_gemm<Half16, CfgSmall>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
+  }
+  if (rc) return rc;
   return check_launch("grouped_gemm_kernel");
 }
