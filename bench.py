@@ -37,6 +37,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", default="", help="comma list of c1,c2,c3a,c3b,c4,c5 (profiling runs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a 1 GiB device-to-device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     p.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
                                                      "profiles", "traffic_radix_topk_c2.json"),
                    help="rocprofv3 --pmc summary giving measured HBM bytes per radix launch")
@@ -57,6 +59,43 @@ def gpu_time_ms(fn, steps: int, warmup: int) -> float:
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def graph_time_ms(fn, calls: int = 20, replays: int = 20) -> float:
+    """Average ms per call with `calls` calls captured in one HIP graph and the
+    graph replayed `replays` times: device time without Python/launch overhead."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (calls * replays)
+
+
+def cpu_time_ms(fn, budget_s: float = 2.0) -> float:
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n < 2:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n * 1e3
 
 
 def router_bytes(M, N, K, in_bytes):
@@ -86,6 +125,15 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        # A plain copy of known size: 1 GiB read + 1 GiB written per dispatch.
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": 1 << 30}))
+        return
     only = set(filter(None, args.only.split(",")))
     want = (lambda c: not only or c in only)
     secondary = {}
@@ -108,12 +156,19 @@ def main():
     for name, (desc, M, N, Kk, bf16) in router_cfgs.items():
         if not want(name):
             continue
-        x = torch.randn(M, N, generator=torch.Generator().manual_seed(0))
-        x = (x.bfloat16() if bf16 else x).to(dev)
+        xc = torch.randn(M, N, generator=torch.Generator().manual_seed(0))
+        xc = xc.bfloat16() if bf16 else xc
+        x = xc.to(dev)
         ms = gpu_time_ms(lambda: K.topk_softmax(x, Kk), args.steps, args.warmup)
+        msg = graph_time_ms(lambda: K.topk_softmax(x, Kk))
         nb = router_bytes(M, N, Kk, 2 if bf16 else 4)
-        secondary[name] = {"workload": desc, "algo": K.select_strategy(N, Kk), "us": ms * 1e3,
-                           "GB_s": nb / ms / 1e6, "frac_hbm": nb / ms / 1e6 / HBM_PEAK_GBS}
+        entry = {"workload": desc, "algo": K.select_strategy(N, Kk), "us_eager": ms * 1e3,
+                 "us": msg * 1e3, "GB_s": nb / msg / 1e6, "frac_hbm": nb / msg / 1e6 / HBM_PEAK_GBS,
+                 "timing": "us: HIP-graph replay (device time); us_eager: Python call loop"}
+        if not args.no_cpu:
+            from oracle import torch_baseline as tb
+            entry["cpu_us"] = cpu_time_ms(lambda: tb.topk_softmax_fused(xc, Kk)) * 1e3
+        secondary[name] = entry
 
     # ---------------- grouped GEMM configs ----------------
     def gemm_cfg(name, desc, T, H, I, E, topk, skew):
@@ -131,15 +186,24 @@ def main():
             W[e0:e1] = (0.02 * torch.randn(e1 - e0, I, H, generator=gc, device=dev)).bfloat16()
         idx = idx.to(dev)
         steps = max(5, min(args.steps, 50 if skew else args.steps))
-        ms = gpu_time_ms(lambda: K.grouped_gemm(X, W, idx), steps, min(args.warmup, 5))
+        ms_eager = gpu_time_ms(lambda: K.grouped_gemm(X, W, idx), steps, min(args.warmup, 5))
+        ms = graph_time_ms(lambda: K.grouped_gemm(X, W, idx), calls=5 if skew else 20,
+                           replays=4 if skew else 20)
         R = T * topk
         flops = 2.0 * R * H * I
         e_nz = int((torch.bincount(idx.flatten(), minlength=E) > 0).sum())
         nbytes = e_nz * I * H * 2 + T * H * 2 + R * I * 2 + R * 4
         tf = flops / ms / 1e9
-        secondary[name] = {"workload": desc, "ms": ms, "TFLOP_s": tf, "frac_mfma": tf / BF16_PEAK_TFLOPS,
+        secondary[name] = {"workload": desc, "ms": ms, "ms_eager": ms_eager, "TFLOP_s": tf,
+                           "frac_mfma": tf / BF16_PEAK_TFLOPS,
                            "GB_s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS,
-                           "rows": R, "experts_nonempty": e_nz}
+                           "rows": R, "experts_nonempty": e_nz,
+                           "timing": "ms: HIP-graph replay of the whole call (routing sort + GEMM)"}
+        if not args.no_cpu and not skew:
+            from oracle import torch_baseline as tb
+            Xc, Wc, ic = X.cpu(), W.cpu(), idx.cpu()
+            secondary[name]["cpu_ms"] = cpu_time_ms(
+                lambda: tb.grouped_gemm_loop(Xc.repeat_interleave(topk, 0), Wc, ic.flatten()), 3.0)
         del W, X
 
     if want("c4"):

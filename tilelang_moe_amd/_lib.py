@@ -65,6 +65,43 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+def current_stream(dev) -> int:
+    """Raw hipStream_t of torch's current stream on `dev` (fast path via
+    torch's internal accessor when present)."""
+    import torch
+
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return raw(idx)
+    return torch.cuda.current_stream(idx).cuda_stream
+
+
+_ws_cache = {}
+_ws_lock = threading.Lock()
+
+
+def workspace(dev, stream: int, nbytes: int):
+    """Device workspace of at least `nbytes` for calls on (`dev`, `stream`).
+
+    Calls on one stream are ordered, so they may share one buffer; calls on
+    different streams get different buffers.  The buffer only grows.  It is
+    zero-initialised once, as the C ABI requires."""
+    import torch
+
+    if nbytes == 0:
+        return None
+    key = (dev.index, stream)
+    buf = _ws_cache.get(key)
+    if buf is None or buf.numel() < nbytes:
+        with _ws_lock:
+            buf = _ws_cache.get(key)
+            if buf is None or buf.numel() < nbytes:
+                buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
+                _ws_cache[key] = buf
+    return buf
+
+
 def check(rc: int) -> None:
     """Turn a C-ABI return code into the reference's exception style."""
     if rc == MOE_OK:

@@ -282,21 +282,23 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
   const int NG = (ntn + SN - 1) / SN;
   const int n_tiles = meta[0];
   const int n_super_raw = (n_tiles + SM - 1) / SM * NG * SUPER;
-  const bool by_super_raw = n_super_raw / SUPER >= 16;
+  // Super-tile order needs the persistent grid and enough super-tiles to
+  // keep every XCD busy for a few rounds.
+  const bool by_super_raw = gridDim.x == 8 * SUPER && n_super_raw / SUPER >= 16;
   // Length of the tile part of the list: padded to whole super-tiles when
   // ordered by super-tile, exact otherwise.
   const int n_super_items = by_super_raw ? n_super_raw : n_tiles * ntn;
   const int64_t n_bad = R - offsets[E];
   const int n_zero = (int)((n_bad + BM - 1) / BM) * ntn;
   const int total = n_super_items + n_zero;
-  // Too few super-tiles to occupy every XCD (small problems): give each XCD
-  // one contiguous eighth of the list instead, walked SUPER items at a time.
+  // Otherwise (small problems) each XCD takes one contiguous eighth of the
+  // list, its gridDim.x / 8 workgroups walking it in strides.
   const bool by_super = by_super_raw;
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int share = (total + 7) >> 3;
   int w = by_super ? xcd * SUPER + slot : xcd * share + slot;
   const int w_end = by_super ? total : min(total, (xcd + 1) * share);
-  const int step = by_super ? gridDim.x : SUPER;
+  const int step = by_super ? (int)gridDim.x : (int)(gridDim.x >> 3);
   for (; w < w_end; w += step) {
   __syncthreads();  // the previous tile's LDS reads are done
   if (w >= n_super_items) {
@@ -531,8 +533,11 @@ static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, uin
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cfg::LDS_BYTES));
     attr_set = true;
   }
-  // Persistent grid: SUPER workgroups per XCD (8 XCDs x 32 CUs x MINB).
-  grouped_gemm_kernel<T, Cfg, MODE><<<dim3(8 * Cfg::SUPER), Cfg::THREADS, Cfg::LDS_BYTES, st>>>(
+  // Persistent grid of SUPER workgroups per XCD (8 XCDs x 32 CUs x MINB) when
+  // the tile list can be long; otherwise one workgroup per possible tile.
+  const int64_t ub = ((R + Cfg::BM - 1) / Cfg::BM + E + 1) * ntn;  // tiles, upper bound
+  const int64_t grid = ub >= 16 * Cfg::SUPER ? 8 * Cfg::SUPER : (ub + 7) / 8 * 8;
+  grouped_gemm_kernel<T, Cfg, MODE><<<dim3((unsigned)grid), Cfg::THREADS, Cfg::LDS_BYTES, st>>>(
       x, w, y, H, I, topk, R, E, ntn, sorted, offsets, t_exp, t_ms, meta);
   return MOE_OK;
 }

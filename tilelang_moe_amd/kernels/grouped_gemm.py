@@ -26,11 +26,6 @@ _DTYPES = {torch.bfloat16: _lib.MOE_BF16, torch.float16: _lib.MOE_F16}
 _IDX = {torch.int32: _lib.MOE_I32, torch.int64: _lib.MOE_I64}
 
 
-def _stream(dev: torch.device) -> int:
-    with torch.cuda.device(dev):
-        return torch.cuda.current_stream(dev).cuda_stream
-
-
 def _check_ids(expert_indices: torch.Tensor, dev: torch.device) -> torch.Tensor:
     if not isinstance(expert_indices, torch.Tensor):
         raise TypeError("expert_indices must be a torch.Tensor")
@@ -81,11 +76,12 @@ def grouped_gemm(X: torch.Tensor, W: torch.Tensor, expert_indices: torch.Tensor)
     if R == 0 or topk == 0:
         return Y
     L = _lib.lib()
+    stream = _lib.current_stream(X.device)
     ws_bytes = L.moe_grouped_gemm_workspace_size(T, topk, E, I)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=X.device)
+    ws = _lib.workspace(X.device, stream, ws_bytes)
     _lib.check(L.moe_grouped_gemm(X.data_ptr(), W.data_ptr(), ids.data_ptr(), _DTYPES[X.dtype],
                                   _IDX[ids.dtype], T, topk, H, I, E, Y.data_ptr(), ws.data_ptr(),
-                                  ws_bytes, _stream(X.device)))
+                                  ws_bytes, stream))
     return Y
 
 
@@ -112,9 +108,10 @@ def route_sort(expert_indices: torch.Tensor, num_experts: int
     offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
     sorted_rows = torch.empty(R, dtype=torch.int32, device=dev)
     L = _lib.lib()
+    stream = _lib.current_stream(dev)
     ws_bytes = L.moe_route_sort_workspace_size(R, E)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    ws = _lib.workspace(dev, stream, ws_bytes)
     _lib.check(L.moe_route_sort(ids.data_ptr(), _IDX[ids.dtype], R, E, counts.data_ptr(),
-                                offsets.data_ptr(), sorted_rows.data_ptr(), ws.data_ptr(), ws_bytes,
-                                _stream(dev)))
+                                offsets.data_ptr(), sorted_rows.data_ptr(),
+                                ws.data_ptr() if ws is not None else None, ws_bytes, stream))
     return counts, offsets, sorted_rows

@@ -71,10 +71,9 @@ def _run(logits: torch.Tensor, k: int, algo: int, with_scores: bool,
     if m == 0:
         return scores, indices
     L = _lib.lib()
+    stream = _lib.current_stream(dev)
     ws_bytes = L.moe_topk_softmax_workspace_size(m, n, k, algo)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
+    ws = _lib.workspace(dev, stream, ws_bytes)
     _lib.check(L.moe_topk_softmax(
         logits.data_ptr(), _LOGIT_DTYPES[logits.dtype], m, n, logits.stride(0), k,
         scores.data_ptr() if with_scores else None, indices.data_ptr(), _IDX_DTYPES[index_dtype],
