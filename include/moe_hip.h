@@ -19,11 +19,13 @@
  *   - Return value: 0 on success, a negative MOE_E* code on failure; the
  *     message of the last failure on the calling thread is moe_last_error().
  *   - Workspaces are caller-owned device buffers of at least the size the
- *     matching *_workspace_size() function returns.  A workspace must be
- *     all-zero before its first use; every entry point leaves it all-zero
- *     again when it returns successfully, so a workspace can be reused by
- *     consecutive calls on ONE stream.  Calls that overlap in time must use
- *     different workspaces.
+ *     matching *_workspace_size() function returns.  Its first 4096 bytes
+ *     are a control block (per-row counters of the split-row top-k) that
+ *     must be all-zero before the first call; every entry point leaves that
+ *     block all-zero when it returns successfully.  The bytes after it are
+ *     scratch that any call overwrites.  So one workspace, zeroed once, can
+ *     serve consecutive calls of any entry point on ONE stream.  Calls that
+ *     overlap in time must use different workspaces.
  */
 #ifndef MOE_HIP_H
 #define MOE_HIP_H

@@ -116,6 +116,38 @@ def test_infinities_and_nan(cuda):
             check(x[:, :n].contiguous(), 4, algo, scores_nan_ok=True)
 
 
+@pytest.mark.parametrize("m,n,k", [(8, 40000, 100), (64, 65536, 2048), (3, 65536, 512), (17, 50000, 4096),
+                                   (2, 300000, 16), (256, 32769, 64), (5, 1 << 20, 8)])
+def test_split_rows(cuda, m, n, k):
+    """Rows longer than one workgroup's registers hold: several workgroups
+    share a row (split-row radix)."""
+    g = torch.Generator(device="cpu").manual_seed(n + k)
+    x = torch.randn(m, n, generator=g)
+    x[0, 5] = float("nan")
+    x[0, 77] = float("inf")
+    x[1 % m, :] = 0.0
+    x[1 % m, ::5] = -0.0
+    x[2 % m, 1000:] = x[2 % m, 1000]  # long run of ties
+    x = x.to(cuda)
+    for _ in range(3):  # the row counters of the workspace must come back to zero
+        check(x, k, "radix", scores_nan_ok=True)
+    check(x.bfloat16(), min(k, 64), "radix", scores_nan_ok=True)
+
+
+def test_workspace_shared_across_calls(cuda):
+    """Split-row calls of different row counts and a grouped GEMM share one
+    workspace on one stream; each must find the control block zeroed."""
+    g = torch.Generator(device="cpu").manual_seed(11)
+    xs = {m: torch.randn(m, 40000, generator=g).to(cuda) for m in (4, 16, 64, 32)}
+    X = torch.randn(256, 512, generator=g).bfloat16().to(cuda)
+    W = torch.randn(8, 256, 512, generator=g).bfloat16().to(cuda)
+    ids = torch.randint(0, 8, (256,), generator=g).int().to(cuda)
+    for m in (4, 16, 64, 32, 4, 64):
+        check(xs[m], 2048, "radix")
+        K.grouped_gemm(X, W, ids)
+    check(xs[64], 1000, "radix")
+
+
 def test_strided_rows_and_int64(cuda):
     g = torch.Generator(device="cpu").manual_seed(3)
     base = torch.randn(50, 1200, generator=g).to(cuda)

@@ -26,6 +26,11 @@ int check_launch(const char* what);
   } while (0)
 
 constexpr int kWave = 64;
+// Every workspace starts with a control block of this size: the only bytes
+// that must be zero before a call, and every call leaves them zero.  Scratch
+// follows it and is overwritten freely, so one workspace can serve every
+// entry point in turn on one stream.
+constexpr size_t kWsCtlBytes = 4096;
 
 // Phase timestamps for kernel tuning builds (-DMOE_PHASE_TIMING): thread 0
 // of each workgroup records the wall clock into moe_phase[block][slot].

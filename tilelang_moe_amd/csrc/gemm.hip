@@ -548,7 +548,7 @@ using namespace moe;
 
 extern "C" size_t moe_route_sort_workspace_size(int64_t R, int64_t E) {
   if (R < 0 || E < 1) return 0;
-  return route_scratch_bytes(R, E);
+  return kWsCtlBytes + route_scratch_bytes(R, E);
 }
 
 extern "C" int moe_route_sort(const void* expert_ids, int idx_dtype, int64_t R, int64_t E,
@@ -560,12 +560,12 @@ extern "C" int moe_route_sort(const void* expert_ids, int idx_dtype, int64_t R, 
     return fail(MOE_EINVAL, "route_sort: expert ids must be int32 or int64");
   if (!counts || !offsets || (R > 0 && (!expert_ids || !sorted_rows)))
     return fail(MOE_EINVAL, "route_sort: null pointer");
-  const size_t need = route_scratch_bytes(R, E);
+  const size_t need = kWsCtlBytes + route_scratch_bytes(R, E);
   if (ws_bytes < need || !workspace)
     return fail(MOE_EINVAL, "route_sort: workspace too small (" + std::to_string(ws_bytes) + " < " +
                                 std::to_string(need) + ")");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  int32_t* blockcnt = static_cast<int32_t*>(workspace);
+  int32_t* blockcnt = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + kWsCtlBytes);
   if (idx_dtype == MOE_I64)
     return launch_route(static_cast<const int64_t*>(expert_ids), R, (int)E, blockcnt, counts, offsets,
                         sorted_rows, 0, nullptr, nullptr, nullptr, st);
@@ -576,7 +576,7 @@ extern "C" int moe_route_sort(const void* expert_ids, int idx_dtype, int64_t R, 
 extern "C" size_t moe_grouped_gemm_workspace_size(int64_t T, int64_t topk, int64_t E, int64_t I) {
   (void)I;
   if (T < 0 || topk < 1 || E < 1) return 0;
-  return gemm_layout(T * topk, E).total;
+  return kWsCtlBytes + gemm_layout(T * topk, E).total;
 }
 
 extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert_ids, int dtype,
@@ -598,11 +598,11 @@ extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert
   if (((uintptr_t)X | (uintptr_t)W) & 15)
     return fail(MOE_EINVAL, "grouped_gemm: X and W must be 16-byte aligned");
   const GemmLayout g = gemm_layout(R, E);
-  if (!workspace || ws_bytes < g.total)
+  if (!workspace || ws_bytes < kWsCtlBytes + g.total)
     return fail(MOE_EINVAL, "grouped_gemm: workspace too small (" + std::to_string(ws_bytes) + " < " +
-                                std::to_string(g.total) + ")");
+                                std::to_string(kWsCtlBytes + g.total) + ")");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
+  char* ws = static_cast<char*>(workspace) + kWsCtlBytes;
   int32_t* blockcnt = reinterpret_cast<int32_t*>(ws + g.blockcnt);
   int32_t* counts = reinterpret_cast<int32_t*>(ws + g.counts);
   int32_t* offsets = reinterpret_cast<int32_t*>(ws + g.offsets);

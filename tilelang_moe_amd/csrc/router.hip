@@ -322,31 +322,27 @@ template <> struct VecLoad<Half16, 8> {
   }
 };
 
-// Row in VGPRs.  Thread t holds KPT keys: vector j (j < KPT/VEC) covers
-// columns VEC*(t + 1024*j) .. +VEC-1, so column order is (j, t, c).
+// ---------------------------------------------------------------------------
+// Pieces shared by the radix kernels.
 //
-// Selection.  A sample of one key per thread, spread over the whole row,
-// gives a lower bound L on the K-th largest key: two radix passes over the
-// sample find the bin of its m-th largest key, m = mu + 4 sigma + 2 with
-// mu = 1024 K / N, and L is that bin's lower edge.  Every key >= L is a
-// candidate.  If that yields fewer than K or more than kCandCap candidates
-// (a skewed row), the exact radix passes over all keys find the threshold
-// key T and the candidates become exactly the K winners (keys above T plus
-// the lowest-column copies of T).
+// Selection.  A sample of 1024 keys spread over the whole row gives a lower
+// bound L on the K-th largest key: a radix pass over the sample finds the
+// bin holding its m-th largest key, m = mu + 4 sigma + 2 with
+// mu = 1024 K / N, and L is that bin's lower edge (one more pass narrows
+// the bin when it would admit too many candidates).  Every key >= L is a
+// candidate.  If the bound admits fewer than K or more than kCandCap
+// candidates (a skewed row), exact radix passes over all keys find the
+// threshold key T instead and exactly K candidates are taken (keys above T,
+// then the lowest-column copies of T).
 //
-// Extraction.  Each thread marks its candidate slots in a bitmask; a block
-// prefix sum of the popcounts gives every candidate its LDS slot, and the
-// extraction loop runs only as many times as the wave's largest popcount,
-// re-reading each candidate's column from L2 (the row was just read) rather
-// than indexing the VGPR array dynamically.  The same loop counts the
-// candidates into kOrdBuckets buckets of (key - base) >> s.
-//
-// Ordering.  Bucket counts are scanned, candidates are scattered bucket by
-// bucket, and each candidate's rank is its bucket start plus the number of
-// larger composites in its bucket.  The thread that ranks a winner (rank <
-// K) also computes its exp and, after one block reduction, stores its score
-// and index.  A bucket holding more than kBucketFixMax candidates switches
-// the row to an LDS bitonic sort.
+// Ordering.  Candidates are counted into kOrdBuckets buckets of
+// (key - base) >> s (base = smallest candidate key), the counts are
+// scanned, candidates are scattered bucket by bucket, and a candidate's rank
+// is its bucket start plus the number of larger composites in its bucket.
+// The thread that ranks a winner (rank < K) also computes its exp and,
+// after one block reduction, stores its score and index.  A bucket holding
+// more than kBucketFixMax candidates switches to an LDS bitonic sort.
+// ---------------------------------------------------------------------------
 constexpr int kCandCap = 8192;
 constexpr int kOrdBuckets = 2048;
 constexpr int kSample = kRadixThreads;
@@ -363,23 +359,274 @@ __device__ inline void wave_aggregated_add(uint32_t* hist, uint32_t bin, bool va
   if (valid && (uint32_t)(__ffsll((long long)match) - 1) == lane) atomicAdd(&hist[bin], (uint32_t)__popcll(match));
 }
 
+// Lower bound L (>= 1) on the K-th largest key of a row of N keys from one
+// sample key per thread.  Deterministic: every workgroup that passes the
+// same samples gets the same L.  hist needs kRadixBins entries.
+__device__ inline uint32_t sample_bound(uint32_t samp, int K, int N, uint32_t* hist, uint32_t* s_pick) {
+  const float mu = (float)kSample * (float)K / (float)N;
+  const float sd = sqrtf(mu * (1.0f - (float)K / (float)N));
+  const int m_rank = (int)ceilf(mu + 4.0f * sd + 2.0f);
+  if (m_rank >= kSample) return 1u;  // no useful bound: every real key
+  const int tid = threadIdx.x;
+  for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
+  __syncthreads();
+  wave_aggregated_add(hist, samp >> 21, true, 11);
+  __syncthreads();
+  RadixState ss{0u, 0u, (uint32_t)m_rank, 0u, false};
+  radix_pick_bin_w0(ss, hist, 21, 0x7FFu, s_pick);
+  // Samples at or above the bin's lower edge estimate the candidate count.
+  const uint32_t at_or_above = (uint32_t)m_rank - ss.need + ss.eq_count;
+  if (!ss.all_taken && (float)at_or_above * ((float)N / kSample) > 0.5f * kCandCap) {
+    for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
+    __syncthreads();
+    const bool in = (samp & ss.fixed) == ss.prefix;
+    if (__ballot(in)) wave_aggregated_add(hist, (samp >> 10) & 0x7FFu, in, 11);
+    __syncthreads();
+    radix_pick_bin_w0(ss, hist, 10, 0x7FFu, s_pick);
+  }
+  return max(ss.prefix, 1u);
+}
+
+// Orders the C candidates in cand[] (LDS, distinct composites, the K largest
+// among them are the row's winners), applies the softmax and stores row
+// `row`.  tmp needs kCandCap entries, hist and bstart kOrdBuckets + 1.
+template <typename IdxT>
+__device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uint32_t rmax, int K,
+                                       int64_t row, uint64_t* tmp, uint32_t* hist, uint32_t* bstart,
+                                       uint32_t* wsum, uint32_t* s_flag, float* s_red,
+                                       float* scores, IdxT* indices) {
+  constexpr int CPT = kCandCap / kRadixThreads;  // candidates per thread, max
+  constexpr int BPT = kOrdBuckets / kRadixThreads;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  int sh = 0;
+  while (((rmax - base) >> sh) >= (uint32_t)kOrdBuckets) ++sh;
+  auto bucket = [&](uint64_t v) { return kOrdBuckets - 1 - (int)((comp_key(v) - base) >> sh); };
+  MOE_PHASE(8);
+  for (int b = tid; b < kOrdBuckets; b += kRadixThreads) hist[b] = 0;
+  if (tid == 0) *s_flag = 0;
+  __syncthreads();
+  for (int p = tid; p < C; p += kRadixThreads) atomicAdd(&hist[bucket(cand[p])], 1u);
+  __syncthreads();
+  MOE_PHASE(9);
+  {
+    uint32_t h[BPT], hs = 0, hmax = 0;
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+      h[q] = hist[tid * BPT + q];
+      hs += h[q];
+      hmax = max(hmax, h[q]);
+    }
+    uint32_t run = block_excl_scan_1024(hs, wsum, nullptr);
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+      bstart[tid * BPT + q] = run;
+      hist[tid * BPT + q] = run;  // cursor
+      run += h[q];
+    }
+    if (tid == 0) bstart[kOrdBuckets] = (uint32_t)C;
+    hmax = wave_max_u32(hmax);
+    if (lane == 0 && hmax > (uint32_t)kBucketFixMax) *s_flag = 1;
+  }
+  __syncthreads();
+  MOE_PHASE(10);
+  if (*s_flag) {
+    // Crowded bucket: sort all candidates instead.
+    const int Cpad = next_pow2_dev(C);
+    for (int p = C + tid; p < Cpad; p += kRadixThreads) cand[p] = 0;
+    __syncthreads();
+    lds_bitonic_desc(cand, Cpad);
+    radix_epilogue(cand, K, row, s_red, scores, indices);
+    return;
+  }
+  for (int p = tid; p < C; p += kRadixThreads) {
+    const uint64_t v = cand[p];
+    tmp[atomicAdd(&hist[bucket(v)], 1u)] = v;
+  }
+  __syncthreads();
+  MOE_PHASE(11);
+  const float vmax = value_of_key(rmax);
+  int rk[CPT];
+  float ex[CPT];
+  uint32_t ix[CPT];
+  float part = 0.0f;
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int p = tid + kRadixThreads * u;
+    rk[u] = K;
+    if (p < C) {
+      const uint64_t v = tmp[p];
+      const int rb = bucket(v);
+      const int beg = (int)bstart[rb], end = (int)bstart[rb + 1];
+      int r = beg;
+      for (int q = beg; q < end; ++q) r += tmp[q] > v;
+      rk[u] = r;
+      ix[u] = comp_idx(v);
+      ex[u] = expf(value_of_key(comp_key(v)) - vmax);
+      if (r < K) part += ex[u];
+    }
+  }
+  MOE_PHASE(12);
+  part = wave_sum_f32(part);
+  if (lane == 0) s_red[tid / kWave] = part;
+  __syncthreads();
+  MOE_PHASE(13);
+  float sum = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kRadixThreads / kWave; ++w) sum += s_red[w];
+#pragma unroll
+  for (int u = 0; u < CPT; ++u)
+    if (rk[u] < K) store_out(scores, indices, row * K + rk[u], ex[u] / sum, ix[u]);
+  MOE_PHASE(14);
+}
+
+// Keys of columns c0 + VEC*(tid + 1024*j) + c, j < KPT/VEC, c < VEC, that lie
+// below `end`; 0 (padding) elsewhere.  All vector loads are issued before any
+// is used: vectors outside the range read the row start instead (always in
+// bounds) and are discarded, so there is no branch, and no wait, between the
+// loads.  Keys use the plain sign flip; `special` reports NaN or -0.0, for
+// which the caller re-keys with key_of_bits.
+template <typename T, int VEC, int KPT>
+__device__ inline void load_keys(const T* __restrict__ x, int c0, int end, uint32_t* key, bool& special) {
+  constexpr int NV = KPT / VEC;
+  const int tid = threadIdx.x;
+  uint32_t bits[KPT];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = c0 + VEC * (tid + kRadixThreads * j);
+    VecLoad<T, VEC>::load(x + (c + VEC <= end ? c : 0), bits + j * VEC);
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = c0 + VEC * (tid + kRadixThreads * j);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const uint32_t b = bits[j * VEC + i];
+      special |= __builtin_amdgcn_classf(__uint_as_float(b), 0x23);  // NaN or -0
+      key[j * VEC + i] = c + VEC <= end ? key_fast(b) : 0u;
+    }
+  }
+  // A vector straddling `end` (end - c0 not a multiple of VEC).
+  if ((end - c0) % VEC != 0) {
+    const int jt = ((end - c0) / VEC) / kRadixThreads, tt = ((end - c0) / VEC) % kRadixThreads;
+    if (tid == tt && jt < NV) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+        if (j == jt)
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            const int c = c0 + VEC * (tid + kRadixThreads * j) + i;
+            if (c < end) {
+              const uint32_t b = Elem<T>::bits(x + c);
+              special |= __builtin_amdgcn_classf(__uint_as_float(b), 0x23);
+              key[j * VEC + i] = key_fast(b);
+            }
+          }
+    }
+  }
+}
+
+template <int KPT>
+__device__ inline void rekey_if_special(uint32_t* key, bool special) {
+  if (__syncthreads_or(special)) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) key[i] = key[i] ? key_of_bits(bits_of_fast_key(key[i])) : 0u;  // 0 = padding
+  }
+}
+
+// Sample key of thread tid for a row of N columns: column floor(tid*N/1024)
+// (exact key; identical in every workgroup of the row).
+template <typename T>
+__device__ inline uint32_t sample_key(const T* __restrict__ x, int N) {
+  const int c = (int)(((int64_t)threadIdx.x * N) / kSample);
+  return key_of_bits(Elem<T>::bits(x + c));
+}
+
+// Whole-row exact path for one workgroup, re-reading the row from L2 in
+// every pass: radix passes find the threshold, then the winners are
+// bitonic-sorted in LDS.  sbuf needs Kpad entries.
+template <typename T, typename IdxT>
+__device__ inline void radix_row_global(const T* __restrict__ x, int64_t N, int K, int Kpad, int64_t row,
+                                        uint64_t* sbuf, uint32_t* hist, uint32_t* wsum, uint32_t* s_pick,
+                                        uint32_t* s_slot, float* s_red, float* scores, IdxT* indices) {
+  const int tid = threadIdx.x;
+  RadixState st{0u, 0u, (uint32_t)K, 0u, false};
+  const int shifts[3] = {21, 10, 0};
+  const uint32_t dmask[3] = {0x7FFu, 0x7FFu, 0x3FFu};
+  for (int pass = 0; pass < 3 && !st.all_taken; ++pass) {
+    for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
+    __syncthreads();
+    for (int64_t i = tid; i < N; i += kRadixThreads) {
+      const uint32_t key = key_of_bits(Elem<T>::bits(x + i));
+      if ((key & st.fixed) == st.prefix) atomicAdd(&hist[(key >> shifts[pass]) & dmask[pass]], 1u);
+    }
+    __syncthreads();
+    radix_pick_bin(st, hist, shifts[pass], dmask[pass], wsum, s_pick);
+  }
+  // Selection rule: key > thr, or key == thr among the first `need` by index.
+  // When a whole bin is taken, every key with the decided digits == prefix
+  // qualifies: express that as "masked key >= prefix".
+  if (tid == 0) *s_slot = 0;
+  __syncthreads();
+  const bool ties_partial = !st.all_taken && st.eq_count > st.need;
+  for (int64_t i = tid; i < N; i += kRadixThreads) {
+    const uint32_t key = key_of_bits(Elem<T>::bits(x + i));
+    const uint32_t mk = key & st.fixed;
+    const bool take = ties_partial ? (mk > st.prefix) : (mk >= st.prefix);
+    if (take) {
+      const uint32_t s = atomicAdd(s_slot, 1u);
+      if (s < (uint32_t)Kpad) sbuf[s] = make_comp(key, (uint32_t)i);
+    }
+  }
+  if (ties_partial) {
+    // The threshold key T = prefix occurs eq_count > need times: take the
+    // `need` lowest indices.  Thread t scans a contiguous index range so the
+    // block prefix sum of per-thread counts orders the copies by index.
+    const int64_t chunk = (N + kRadixThreads - 1) / kRadixThreads;
+    const int64_t lo = std::min<int64_t>(N, tid * chunk), hi = std::min<int64_t>(N, lo + chunk);
+    uint32_t cnt = 0;
+    for (int64_t i = lo; i < hi; ++i) cnt += key_of_bits(Elem<T>::bits(x + i)) == st.prefix;
+    uint32_t before = block_excl_scan_1024(cnt, wsum, nullptr);
+    for (int64_t i = lo; i < hi && before < st.need; ++i) {
+      const uint32_t key = key_of_bits(Elem<T>::bits(x + i));
+      if (key == st.prefix) {
+        const uint32_t s = atomicAdd(s_slot, 1u);
+        if (s < (uint32_t)Kpad) sbuf[s] = make_comp(key, (uint32_t)i);
+        ++before;
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = K + tid; i < Kpad; i += kRadixThreads) sbuf[i] = 0;
+  __syncthreads();
+  lds_bitonic_desc(sbuf, Kpad);
+  radix_epilogue(sbuf, K, row, s_red, scores, indices);
+}
+
+// ===========================================================================
+// 3a. One workgroup per row, row in VGPRs (N <= 32K with 16-byte rows).
+//     Thread t holds KPT keys: vector j covers columns VEC*(t + 1024*j) ..
+//     +VEC-1, so column order is (j, t, c).  Candidate extraction: each
+//     thread marks its candidate slots in a bitmask, a block prefix sum of
+//     the popcounts gives every candidate its LDS slot, and the extraction
+//     loop runs only as many times as the wave's largest popcount, re-reading
+//     each candidate's column from L2 (the row was just read) instead of
+//     indexing the VGPR array dynamically.
+// ===========================================================================
 template <typename T, typename IdxT, int VEC, int KPT>
 __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
     const T* __restrict__ logits, int64_t M, int N, int64_t ld, int K, int Kpad,
     float* __restrict__ scores, IdxT* __restrict__ indices) {
   static_assert(KPT <= 32, "candidate bitmask is 32 bits");
   constexpr int NV = KPT / VEC;
-  constexpr int CPT = kCandCap / kRadixThreads;  // candidates per thread, max
   extern __shared__ uint64_t dyn[];
   uint64_t* cand = dyn;              // [kCandCap] in extraction order
   uint64_t* tmp = dyn + kCandCap;    // [kCandCap] grouped by bucket
-  __shared__ uint32_t hist[kRadixBins];  // radix digits; bucket counts and cursors
+  __shared__ uint32_t hist[kRadixBins + 1];
   __shared__ uint32_t bstart[kOrdBuckets + 1];
   __shared__ uint32_t wsum[kRadixThreads / kWave];
   __shared__ uint32_t s_pick[3];
-  __shared__ uint32_t s_max, s_hmax;
+  __shared__ uint32_t s_max, s_flag;
   __shared__ float s_red[kRadixThreads / kWave];
-  static_assert(kOrdBuckets <= kRadixBins, "bucket counts live in hist[]");
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -387,94 +634,24 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   const T* x = logits + row * ld;
 
   MOE_PHASE(0);
-  // ---- load the row once; key 0 marks columns past N ----
-  // Keys are first formed with the plain sign flip; rows holding a NaN or a
-  // -0.0 (flagged by v_cmp_class) are re-keyed with key_of_bits below.
   uint32_t key[KPT];
   bool special = false;
-  {
-    // All vector loads are issued before any is used: out-of-row vectors
-    // read the row's first vector instead (always in bounds) and are
-    // discarded, so there is no branch, and no wait, between the loads.
-    uint32_t bits[KPT];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int c0 = VEC * (tid + kRadixThreads * j);
-      VecLoad<T, VEC>::load(x + (c0 + VEC <= N ? c0 : 0), bits + j * VEC);
-    }
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int c0 = VEC * (tid + kRadixThreads * j);
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        const uint32_t b = bits[j * VEC + c];
-        special |= __builtin_amdgcn_classf(__uint_as_float(b), 0x23);  // NaN or -0
-        key[j * VEC + c] = c0 + VEC <= N ? key_fast(b) : 0u;
-      }
-    }
-    // A vector straddling the row end (N not a multiple of VEC).
-    const int jt = (N / VEC) / kRadixThreads, tt = (N / VEC) % kRadixThreads;
-    if (N % VEC != 0 && tid == tt && jt < NV) {
-#pragma unroll
-      for (int j = 0; j < NV; ++j)
-        if (j == jt)
-#pragma unroll
-          for (int c = 0; c < VEC; ++c)
-            if (VEC * (tid + kRadixThreads * j) + c < N) {
-              const uint32_t b = Elem<T>::bits(x + VEC * (tid + kRadixThreads * j) + c);
-              special |= __builtin_amdgcn_classf(__uint_as_float(b), 0x23);
-              key[j * VEC + c] = key_fast(b);
-            }
-    }
-  }
+  load_keys<T, VEC, KPT>(x, 0, N, key, special);
+  const uint32_t samp = sample_key(x, N);
   MOE_PHASE(1);
-
-  // ---- row maximum; sample bound L ----
-  if (__syncthreads_or(special)) {
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) key[i] = key[i] ? key_of_bits(bits_of_fast_key(key[i])) : 0u;  // 0 = padding
-  }
+  rekey_if_special<KPT>(key, special);
   uint32_t kmax = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) kmax = max(kmax, key[i]);
   kmax = wave_max_u32(kmax);
-  // Sample key: slot q, one per wave (wave-uniform, so a scalar branch),
-  // spread so that the 16 waves cover every vector j.
-  uint32_t samp = 0;
-  {
-    const int q = __builtin_amdgcn_readfirstlane((tid / kWave) * KPT / (kRadixThreads / kWave));
-#pragma unroll
-    for (int i = 0; i < KPT; ++i)
-      if (q == i) samp = key[i];
-  }
   if (tid == 0) s_max = 0;
-  for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
   __syncthreads();
   if (lane == 0) atomicMax(&s_max, kmax);
-  const float mu = (float)kSample * (float)K / (float)N;
-  const float sd = sqrtf(mu * (1.0f - (float)K / (float)N));
-  const int m_rank = (int)ceilf(mu + 4.0f * sd + 2.0f);
-  uint32_t L = 1u;  // 1: every real key (0 is padding)
-  if (m_rank < kSample) {
-    RadixState ss{0u, 0u, (uint32_t)m_rank, 0u, false};
-    wave_aggregated_add(hist, samp >> 21, true, 11);
-    __syncthreads();
-    radix_pick_bin_w0(ss, hist, 21, 0x7FFu, s_pick);
-    MOE_PHASE(2);
-    if (!ss.all_taken) {
-      for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
-      __syncthreads();
-      const bool in = (samp & ss.fixed) == ss.prefix;
-      if (__ballot(in)) wave_aggregated_add(hist, (samp >> 10) & 0x7FFu, in, 11);
-      __syncthreads();
-      radix_pick_bin_w0(ss, hist, 10, 0x7FFu, s_pick);
-    }
-    L = max(ss.prefix, 1u);  // lower edge of the bin of the m-th largest sample
-  }
-  MOE_PHASE(3);
+  const uint32_t L = sample_bound(samp, K, N, hist, s_pick);  // has barriers
+  MOE_PHASE(2);
   const uint32_t rmax = s_max;
 
-  // ---- candidate mask: sample mode (key >= L), else exact mode ----
+  // ---- candidate mask: keys >= L, else exact mode ----
   uint32_t mask = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) mask |= (uint32_t)(key[i] >= L) << i;
@@ -543,14 +720,9 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
     cpos = block_excl_scan_1024((uint32_t)__popc(mask), wsum, &C);  // C == K
     base = st.prefix;
   }
-  int sh = 0;
-  while (((rmax - base) >> sh) >= (uint32_t)kOrdBuckets) ++sh;
-  for (int b = tid; b < kOrdBuckets; b += kRadixThreads) hist[b] = 0;
-  if (tid == 0) s_hmax = 0;
-  __syncthreads();
-  MOE_PHASE(4);
+  MOE_PHASE(3);
 
-  // ---- extraction: candidate columns re-read from L2, bucket counts ----
+  // ---- extraction: candidate columns re-read from L2 ----
   {
     constexpr int BATCH = 4;  // loads in flight per lane
     const uint32_t rounds = wave_max_u32((uint32_t)__popc(mask));
@@ -569,94 +741,164 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
 #pragma unroll
       for (int u = 0; u < BATCH; ++u) bits[u] = Elem<T>::bits(x + (col[u] >= 0 ? col[u] : 0));
 #pragma unroll
+      for (int u = 0; u < BATCH; ++u)
+        if (col[u] >= 0) cand[cpos++] = make_comp(key_of_bits(bits[u]), (uint32_t)col[u]);
+    }
+  }
+  __syncthreads();
+  MOE_PHASE(4);
+  order_and_store(cand, (int)C, base, rmax, K, row, tmp, hist, bstart, wsum, &s_flag, s_red, scores, indices);
+  MOE_PHASE(5);
+}
+
+// ===========================================================================
+// 3b. G workgroups per row (few rows, long rows: e.g. 64 rows of 32K).
+//     Workgroup g loads columns [g*slice, (g+1)*slice) into VGPRs.  All G
+//     workgroups compute the same bound L from the same row-wide sample,
+//     compact their candidates (keys >= L) into the row's global candidate
+//     buffer (one atomic per workgroup reserves the space) and publish their
+//     slice maximum.  The last workgroup to finish (agent-scope release /
+//     exchange through agent-scope atomic stores and loads and a per-row
+//     counter; no workgroup waits for another)
+//     orders the candidates, applies the softmax, stores the row and resets
+//     the row's counters to zero for the next call.  If the bound admitted
+//     fewer than K or more than kCandCap candidates, that last workgroup runs
+//     the exact whole-row path instead.
+//     The G workgroups of a row are numbered so that they land on one XCD
+//     (workgroup b runs on XCD b % 8), which keeps the row's slices in one
+//     L2 for the last workgroup's re-reads; correctness does not depend on it.
+// ===========================================================================
+struct SplitRowCtl {
+  uint32_t count;   // candidates published
+  uint32_t done;    // workgroups finished
+  uint32_t rmax;    // row maximum key
+  uint32_t pad;
+};
+
+template <typename T, typename IdxT, int VEC, int KPT>
+__global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
+    const T* __restrict__ logits, int64_t M, int N, int64_t ld, int K, int Kpad, int G, int slice,
+    float* __restrict__ scores, IdxT* __restrict__ indices, SplitRowCtl* __restrict__ ctl,
+    uint64_t* __restrict__ gcand) {
+  static_assert(KPT <= 32, "candidate bitmask is 32 bits");
+  extern __shared__ uint64_t dyn[];
+  uint64_t* cand = dyn;              // [kCandCap]
+  uint64_t* tmp = dyn + kCandCap;    // [kCandCap]
+  __shared__ uint32_t hist[kRadixBins + 1];
+  __shared__ uint32_t bstart[kOrdBuckets + 1];
+  __shared__ uint32_t wsum[kRadixThreads / kWave];
+  __shared__ uint32_t s_pick[3];
+  __shared__ uint32_t s_max, s_flag, s_base, s_last;
+  __shared__ float s_red[kRadixThreads / kWave];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int q = blockIdx.x >> 3;
+  const int g = q % G;
+  const int64_t row = (int64_t)(q / G) * 8 + (blockIdx.x & 7);
+  if (row >= M) return;  // whole workgroup
+  const T* x = logits + row * ld;
+  SplitRowCtl* rc = ctl + row;
+  uint64_t* rcand = gcand + row * kCandCap;
+  const int c0 = g * slice;
+  const int end = min(N, c0 + slice);
+
+  MOE_PHASE(0);
+  uint32_t key[KPT];
+  bool special = false;
+  load_keys<T, VEC, KPT>(x, c0, end, key, special);
+  const uint32_t samp = sample_key(x, N);
+  MOE_PHASE(1);
+  rekey_if_special<KPT>(key, special);
+  uint32_t kmax = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) kmax = max(kmax, key[i]);
+  kmax = wave_max_u32(kmax);
+  if (tid == 0) s_max = 0;
+  __syncthreads();
+  if (lane == 0) atomicMax(&s_max, kmax);
+  const uint32_t L = sample_bound(samp, K, N, hist, s_pick);  // has barriers
+  MOE_PHASE(2);
+
+  uint32_t mask = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) mask |= (uint32_t)(key[i] >= L) << i;
+  uint32_t cnt;
+  uint32_t cpos = block_excl_scan_1024((uint32_t)__popc(mask), wsum, &cnt);
+  if (tid == 0) {
+    s_base = atomicAdd(&rc->count, cnt);
+    atomicMax(&rc->rmax, s_max);
+  }
+  __syncthreads();
+  cpos += s_base;
+  MOE_PHASE(3);
+  {
+    constexpr int BATCH = 4;
+    const uint32_t rounds = wave_max_u32((uint32_t)__popc(mask));
+    for (uint32_t it = 0; it < rounds; it += BATCH) {
+      int col[BATCH];
+      uint32_t bits[BATCH];
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        col[u] = -1;
+        if (mask) {
+          const int i = __ffs(mask) - 1;
+          mask &= mask - 1;
+          col[u] = c0 + VEC * (tid + kRadixThreads * (i / VEC)) + (i % VEC);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) bits[u] = Elem<T>::bits(x + (col[u] >= 0 ? col[u] : 0));
+#pragma unroll
       for (int u = 0; u < BATCH; ++u) {
         if (col[u] >= 0) {
-          const uint32_t k = key_of_bits(bits[u]);
-          cand[cpos++] = make_comp(k, (uint32_t)col[u]);
-          atomicAdd(&hist[kOrdBuckets - 1 - ((k - base) >> sh)], 1u);
+          if (cpos < (uint32_t)kCandCap)
+            __hip_atomic_store(rcand + cpos, make_comp(key_of_bits(bits[u]), (uint32_t)col[u]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ++cpos;
         }
       }
     }
   }
+  MOE_PHASE(4);
+  // Publish, then count in.  The candidates went out as agent-scope atomic
+  // stores, which write through the XCD's L2, so waiting for this
+  // workgroup's stores to complete is the whole release: no L2 writeback
+  // (an agent-scope release fence writes back the entire L2 of the XCD,
+  // which costs tens of microseconds when every workgroup issues one).
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  {
-    constexpr int BPT = kOrdBuckets / kRadixThreads;
-    uint32_t h[BPT], hs = 0, hmax = 0;
-#pragma unroll
-    for (int q = 0; q < BPT; ++q) {
-      h[q] = hist[tid * BPT + q];
-      hs += h[q];
-      hmax = max(hmax, h[q]);
-    }
-    uint32_t run = block_excl_scan_1024(hs, wsum, nullptr);
-#pragma unroll
-    for (int q = 0; q < BPT; ++q) {
-      bstart[tid * BPT + q] = run;
-      hist[tid * BPT + q] = run;  // cursor
-      run += h[q];
-    }
-    if (tid == 0) bstart[kOrdBuckets] = C;
-    hmax = wave_max_u32(hmax);
-    if (lane == 0) atomicMax(&s_hmax, hmax);
-  }
+  if (tid == 0) s_last = __hip_atomic_fetch_add(&rc->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(G - 1);
   __syncthreads();
   MOE_PHASE(5);
-  for (uint32_t p = tid; p < C; p += kRadixThreads) {
-    const uint64_t v = cand[p];
-    const uint32_t pos = atomicAdd(&hist[kOrdBuckets - 1 - ((comp_key(v) - base) >> sh)], 1u);
-    tmp[pos] = v;
-  }
-  __syncthreads();
-  MOE_PHASE(6);
-  const float vmax = value_of_key(rmax);
+  if (!s_last) return;
 
-  if (s_hmax > (uint32_t)kBucketFixMax) {
-    // Crowded bucket: sort all candidates (C <= kCandCap) instead.
-    const int Cpad = next_pow2_dev((int)C);
-    for (int p = (int)C + tid; p < Cpad; p += kRadixThreads) tmp[p] = 0;
-    __syncthreads();
-    lds_bitonic_desc(tmp, Cpad);
-    radix_epilogue(tmp, K, row, s_red, scores, indices);
-    MOE_PHASE(7);
-    MOE_PHASE(8);
+  // ---- last workgroup of the row ----
+  const uint32_t C = __hip_atomic_load(&rc->count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t rmax = __hip_atomic_load(&rc->rmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (tid == 0) {  // leave the row's counters zeroed for the next call
+    __hip_atomic_store(&rc->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&rc->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&rc->rmax, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (C < (uint32_t)K || C > (uint32_t)kCandCap) {
+    radix_row_global<T, IdxT>(x, N, K, Kpad, row, cand, hist, wsum, s_pick, &s_flag, s_red, scores, indices);
     return;
   }
-
-  // ---- rank within bucket, exp, block sum, store ----
-  int rk[CPT];
-  float ex[CPT];
-  uint32_t ix[CPT];
-  float part = 0.0f;
-#pragma unroll
-  for (int u = 0; u < CPT; ++u) {
-    const uint32_t p = tid + kRadixThreads * u;
-    rk[u] = K;
-    if (p < C) {
-      const uint64_t v = tmp[p];
-      const int rb = kOrdBuckets - 1 - (int)((comp_key(v) - base) >> sh);
-      const int beg = (int)bstart[rb], end = (int)bstart[rb + 1];
-      int r = beg;
-      for (int q = beg; q < end; ++q) r += tmp[q] > v;
-      rk[u] = r;
-      ix[u] = comp_idx(v);
-      ex[u] = expf(value_of_key(comp_key(v)) - vmax);
-      if (r < K) part += ex[u];
-    }
-  }
-  MOE_PHASE(7);
-  part = wave_sum_f32(part);
-  if (lane == 0) s_red[tid / kWave] = part;
+  // Agent-scope atomic loads read past this XCD's L2 copy, so they see every
+  // workgroup's candidates.
+  for (uint32_t p = tid; p < C; p += kRadixThreads)
+    cand[p] = __hip_atomic_load(rcand + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  float sum = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kRadixThreads / kWave; ++w) sum += s_red[w];
-#pragma unroll
-  for (int u = 0; u < CPT; ++u)
-    if (rk[u] < K) store_out(scores, indices, row * K + rk[u], ex[u] / sum, ix[u]);
-  MOE_PHASE(8);
+  MOE_PHASE(6);
+  order_and_store(cand, (int)C, L, rmax, K, row, tmp, hist, bstart, wsum, &s_flag, s_red, scores, indices);
+  MOE_PHASE(7);
 }
 
-// Any N: the row is re-read from global memory (L2) in every pass.
+// ===========================================================================
+// 3c. Any N: one workgroup per row re-reads the row from L2 in every pass.
+// ===========================================================================
 template <typename T, typename IdxT>
 __global__ __launch_bounds__(kRadixThreads) void topk_radix_kernel(
     const T* __restrict__ logits, int64_t M, int64_t N, int64_t ld, int K, int Kpad,
@@ -666,63 +908,9 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_kernel(
   __shared__ uint32_t wsum[kRadixThreads / kWave];
   __shared__ uint32_t s_pick[2], s_slot;
   __shared__ float s_red[kRadixThreads / kWave];
-
-  const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
-  const T* x = logits + row * ld;
-
-  RadixState st{0u, 0u, (uint32_t)K, 0u, false};
-  const int shifts[3] = {21, 10, 0};
-  const uint32_t dmask[3] = {0x7FFu, 0x7FFu, 0x3FFu};
-  for (int pass = 0; pass < 3 && !st.all_taken; ++pass) {
-    for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
-    __syncthreads();
-    for (int64_t i = tid; i < N; i += kRadixThreads) {
-      const uint32_t key = key_of_bits(Elem<T>::bits(x + i));
-      if ((key & st.fixed) == st.prefix) atomicAdd(&hist[(key >> shifts[pass]) & dmask[pass]], 1u);
-    }
-    __syncthreads();
-    radix_pick_bin(st, hist, shifts[pass], dmask[pass], wsum, s_pick);
-  }
-
-  // Selection rule: key > thr, or key == thr among the first `need` by index.
-  // When a whole bin is taken, every key with the decided digits == prefix
-  // qualifies: express that as "masked key >= prefix".
-  if (tid == 0) s_slot = 0;
-  __syncthreads();
-  const bool ties_partial = !st.all_taken && st.eq_count > st.need;
-  for (int64_t i = tid; i < N; i += kRadixThreads) {
-    const uint32_t key = key_of_bits(Elem<T>::bits(x + i));
-    const uint32_t mk = key & st.fixed;
-    const bool take = ties_partial ? (mk > st.prefix) : (mk >= st.prefix);
-    if (take) {
-      const uint32_t s = atomicAdd(&s_slot, 1u);
-      if (s < (uint32_t)Kpad) sbuf[s] = make_comp(key, (uint32_t)i);
-    }
-  }
-  if (ties_partial) {
-    // The threshold key T = prefix occurs eq_count > need times: take the
-    // `need` lowest indices.  Thread t scans a contiguous index range so the
-    // block prefix sum of per-thread counts orders the copies by index.
-    const int64_t chunk = (N + kRadixThreads - 1) / kRadixThreads;
-    const int64_t lo = std::min<int64_t>(N, tid * chunk), hi = std::min<int64_t>(N, lo + chunk);
-    uint32_t cnt = 0;
-    for (int64_t i = lo; i < hi; ++i) cnt += key_of_bits(Elem<T>::bits(x + i)) == st.prefix;
-    uint32_t before = block_excl_scan_1024(cnt, wsum, nullptr);
-    for (int64_t i = lo; i < hi && before < st.need; ++i) {
-      const uint32_t key = key_of_bits(Elem<T>::bits(x + i));
-      if (key == st.prefix) {
-        const uint32_t s = atomicAdd(&s_slot, 1u);
-        if (s < (uint32_t)Kpad) sbuf[s] = make_comp(key, (uint32_t)i);
-        ++before;
-      }
-    }
-  }
-  __syncthreads();
-  for (int i = K + tid; i < Kpad; i += kRadixThreads) sbuf[i] = 0;
-  __syncthreads();
-  lds_bitonic_desc(sbuf, Kpad);
-  radix_epilogue(sbuf, K, row, s_red, scores, indices);
+  radix_row_global<T, IdxT>(logits + row * ld, N, K, Kpad, row, sbuf, hist, wsum, s_pick, &s_slot, s_red,
+                            scores, indices);
 }
 
 // ===========================================================================
@@ -817,11 +1005,93 @@ static int launch_radix_reg_v(const T* x, int64_t M, int N, int64_t ld, int K, f
   return fail(MOE_EUNSUP, "radix row too long for the register kernel");
 }
 
+// Split-row plan: G workgroups per row when rows are few and long, so that
+// about one workgroup per CU is busy.  G == 1: no split.
+static int num_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
+// Rows whose counters fit in the workspace control block.
+constexpr int64_t kSplitMaxRows = kWsCtlBytes / sizeof(SplitRowCtl);
+constexpr int kSplitMaxG = 64;
+
+#ifdef MOE_PHASE_TIMING
+int moe_split_g_override = 0;  // tuning builds only
+#endif
+
+// Rows too long for one workgroup's registers are split over G workgroups
+// (G a power of two, slice <= 1024 * kRadixRegMaxKPT keys).  Rows that fit
+// stay whole: a row is latency-bound, and for them the candidate exchange
+// costs about what the shorter slices save.  G grows further (to slices of
+// 8192 keys) while the grid stays within one workgroup per CU (each
+// workgroup takes 128 KB of LDS).
+static int split_groups(int64_t M, int64_t N, int64_t K) {
+  if (K > kRadixRegMaxK || M < 1 || M > kSplitMaxRows) return 1;
+#ifdef MOE_PHASE_TIMING
+  if (moe_split_g_override) return moe_split_g_override;
+#endif
+  const int64_t cap = (int64_t)kRadixThreads * kRadixRegMaxKPT;
+  if (N <= cap) return 1;
+  int G = 1;
+  while ((int64_t)G * cap < N) G *= 2;
+  if (G > kSplitMaxG) return 1;
+  while (G < kSplitMaxG && N / (2 * G) >= 8192 && M * 2 * G <= (int64_t)num_cus()) G *= 2;
+  return G;
+}
+
+static size_t split_ws_bytes(int64_t M) {
+  return kWsCtlBytes + (size_t)M * kCandCap * sizeof(uint64_t);
+}
+
+template <typename T, typename IdxT, int VEC, int KPT>
+static int launch_radix_split(const T* x, int64_t M, int N, int64_t ld, int K, int G, int slice, float* s,
+                              IdxT* id, void* ws, hipStream_t st) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    MOE_HIP_CHECK(hipFuncSetAttribute((const void*)topk_radix_split_kernel<T, IdxT, VEC, KPT>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)(2 * kCandCap * sizeof(uint64_t))));
+    attr_set = true;
+  }
+  SplitRowCtl* ctl = static_cast<SplitRowCtl*>(ws);
+  uint64_t* gcand = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + kWsCtlBytes);
+  const int64_t grid = (M + 7) / 8 * 8 * G;
+  topk_radix_split_kernel<T, IdxT, VEC, KPT><<<dim3((unsigned)grid), dim3(kRadixThreads),
+                                                2 * kCandCap * sizeof(uint64_t), st>>>(
+      x, M, N, ld, K, next_pow2(K), G, slice, s, id, ctl, gcand);
+  return check_launch("topk_radix_split_kernel");
+}
+
+template <typename T, typename IdxT, int VEC, int KPT>
+static int launch_radix_split_v(const T* x, int64_t M, int N, int64_t ld, int K, int G, int slice, float* s,
+                                IdxT* id, void* ws, hipStream_t st) {
+  if (slice / kRadixThreads <= KPT) return launch_radix_split<T, IdxT, VEC, KPT>(x, M, N, ld, K, G, slice, s, id, ws, st);
+  if constexpr (2 * KPT <= kRadixRegMaxKPT)
+    return launch_radix_split_v<T, IdxT, VEC, 2 * KPT>(x, M, N, ld, K, G, slice, s, id, ws, st);
+  return fail(MOE_EUNSUP, "radix slice too long");
+}
+
 template <typename T, typename IdxT>
 static int launch_radix(const T* x, int64_t M, int64_t N, int64_t ld, int K, float* s, IdxT* id,
-                        hipStream_t st) {
+                        void* ws, size_t ws_bytes, hipStream_t st) {
   constexpr int VEC = 16 / sizeof(T);
   const bool vec_ok = ((uintptr_t)x % 16 == 0) && ((ld * (int64_t)sizeof(T)) % 16 == 0);
+  const int G = split_groups(M, N, K);
+  if (G > 1 && vec_ok && ws && ws_bytes >= split_ws_bytes(M)) {
+    const int64_t unit = (int64_t)VEC * kRadixThreads;
+    const int64_t slice = ((N + G - 1) / G + unit - 1) / unit * unit;
+    if (slice <= (int64_t)kRadixThreads * kRadixRegMaxKPT)
+      return launch_radix_split_v<T, IdxT, VEC, VEC>(x, M, (int)N, ld, K, G, (int)slice, s, id, ws, st);
+  }
   if (K <= kRadixRegMaxK && N <= (int64_t)kRadixThreads * (vec_ok ? kRadixRegMaxKPT : 16)) {
     if (vec_ok) return launch_radix_reg_v<T, IdxT, VEC, VEC>(x, M, (int)N, ld, K, s, id, st);
     return launch_radix_reg_v<T, IdxT, 1, 1>(x, M, (int)N, ld, K, s, id, st);
@@ -842,13 +1112,14 @@ static int launch_radix(const T* x, int64_t M, int64_t N, int64_t ld, int K, flo
 
 template <typename T, typename IdxT>
 static int dispatch_topk(const void* logits, int64_t M, int64_t N, int64_t ld, int64_t K,
-                         float* scores, void* indices, int algo, hipStream_t st) {
+                         float* scores, void* indices, int algo, void* ws, size_t ws_bytes,
+                         hipStream_t st) {
   const T* x = static_cast<const T*>(logits);
   IdxT* id = static_cast<IdxT*>(indices);
   switch (algo) {
     case MOE_TOPK_BITONIC: return launch_bitonic<T, IdxT>(x, M, (int)N, ld, (int)K, scores, id, st);
     case MOE_TOPK_SELECTION: return launch_select<T, IdxT>(x, M, (int)N, ld, (int)K, scores, id, st);
-    case MOE_TOPK_RADIX: return launch_radix<T, IdxT>(x, M, N, ld, (int)K, scores, id, st);
+    case MOE_TOPK_RADIX: return launch_radix<T, IdxT>(x, M, N, ld, (int)K, scores, id, ws, ws_bytes, st);
     default: return fail(MOE_EINVAL, "unknown top-k algorithm");
   }
 }
@@ -865,15 +1136,16 @@ extern "C" int moe_topk_select_algo(int64_t N, int64_t K) {
 }
 
 extern "C" size_t moe_topk_softmax_workspace_size(int64_t M, int64_t N, int64_t K, int algo) {
-  (void)M; (void)N; (void)K; (void)algo;
-  return 0;
+  if (M < 1 || N < 1 || K < 1 || K > N) return 0;
+  if (algo == MOE_TOPK_AUTO) algo = moe_topk_select_algo(N, K);
+  if (algo != MOE_TOPK_RADIX || split_groups(M, N, K) <= 1) return 0;
+  return split_ws_bytes(M);
 }
 
 extern "C" int moe_topk_softmax(const void* logits, int logits_dtype, int64_t M, int64_t N,
                                 int64_t ld, int64_t K, float* scores, void* indices,
                                 int idx_dtype, int algo, void* workspace, size_t ws_bytes,
                                 void* stream) {
-  (void)workspace; (void)ws_bytes;
   if (M < 0 || N < 1 || K < 1 || K > N)
     return fail(MOE_EINVAL, "topk_softmax: need M >= 0, N >= 1 and 1 <= K <= N (got M=" +
                                 std::to_string(M) + ", N=" + std::to_string(N) +
@@ -896,14 +1168,14 @@ extern "C" int moe_topk_softmax(const void* logits, int logits_dtype, int64_t M,
   const bool i64 = idx_dtype == MOE_I64;
   switch (logits_dtype) {
     case MOE_F32:
-      return i64 ? dispatch_topk<float, int64_t>(logits, M, N, ld, K, scores, indices, algo, st)
-                 : dispatch_topk<float, int32_t>(logits, M, N, ld, K, scores, indices, algo, st);
+      return i64 ? dispatch_topk<float, int64_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st)
+                 : dispatch_topk<float, int32_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st);
     case MOE_BF16:
-      return i64 ? dispatch_topk<uint16_t, int64_t>(logits, M, N, ld, K, scores, indices, algo, st)
-                 : dispatch_topk<uint16_t, int32_t>(logits, M, N, ld, K, scores, indices, algo, st);
+      return i64 ? dispatch_topk<uint16_t, int64_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st)
+                 : dispatch_topk<uint16_t, int32_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st);
     case MOE_F16:
-      return i64 ? dispatch_topk<Half16, int64_t>(logits, M, N, ld, K, scores, indices, algo, st)
-                 : dispatch_topk<Half16, int32_t>(logits, M, N, ld, K, scores, indices, algo, st);
+      return i64 ? dispatch_topk<Half16, int64_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st)
+                 : dispatch_topk<Half16, int32_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st);
     default:
       return fail(MOE_EINVAL, "topk_softmax: logits must be float32, bfloat16 or float16");
   }
