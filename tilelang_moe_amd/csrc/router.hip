@@ -479,28 +479,36 @@ __device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uin
   MOE_PHASE(14);
 }
 
-// Keys of columns c0 + VEC*(tid + 1024*j) + c, j < KPT/VEC, c < VEC, that lie
-// below `end`; 0 (padding) elsewhere.  All vector loads are issued before any
-// is used: vectors outside the range read the row start instead (always in
-// bounds) and are discarded, so there is no branch, and no wait, between the
-// loads.  Keys use the plain sign flip; `special` reports NaN or -0.0, for
-// which the caller re-keys with key_of_bits.
+// Row slice [c0, end) of thread tid: columns c0 + VEC*(tid + 1024*j) + c,
+// j < KPT/VEC, c < VEC.  Loading is split in two so that work needing only
+// the row's sample (the bound) runs while these loads are in flight:
+// issue_row_loads starts every vector load and touches none of them (vectors
+// outside the range read the row start instead, always in bounds, so there
+// is no branch between the loads); keys_from_bits later turns the raw bits
+// into keys in place, 0 (padding) outside the range.  Keys use the plain
+// sign flip; `special` reports NaN or -0.0, for which the caller re-keys
+// with key_of_bits.
 template <typename T, int VEC, int KPT>
-__device__ inline void load_keys(const T* __restrict__ x, int c0, int end, uint32_t* key, bool& special) {
+__device__ inline void issue_row_loads(const T* __restrict__ x, int c0, int end, uint32_t* bits) {
   constexpr int NV = KPT / VEC;
   const int tid = threadIdx.x;
-  uint32_t bits[KPT];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = c0 + VEC * (tid + kRadixThreads * j);
     VecLoad<T, VEC>::load(x + (c + VEC <= end ? c : 0), bits + j * VEC);
   }
+}
+
+template <typename T, int VEC, int KPT>
+__device__ inline void keys_from_bits(const T* __restrict__ x, int c0, int end, uint32_t* key, bool& special) {
+  constexpr int NV = KPT / VEC;
+  const int tid = threadIdx.x;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = c0 + VEC * (tid + kRadixThreads * j);
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
-      const uint32_t b = bits[j * VEC + i];
+      const uint32_t b = key[j * VEC + i];
       special |= __builtin_amdgcn_classf(__uint_as_float(b), 0x23);  // NaN or -0
       key[j * VEC + i] = c + VEC <= end ? key_fast(b) : 0u;
     }
@@ -523,6 +531,12 @@ __device__ inline void load_keys(const T* __restrict__ x, int c0, int end, uint3
           }
     }
   }
+}
+
+// Column of key slot i of thread tid in a slice starting at c0.
+template <int VEC>
+__device__ inline uint32_t slot_col(int c0, int i) {
+  return (uint32_t)(c0 + VEC * ((int)threadIdx.x + kRadixThreads * (i / VEC)) + (i % VEC));
 }
 
 template <int KPT>
@@ -634,22 +648,23 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   const T* x = logits + row * ld;
 
   MOE_PHASE(0);
-  uint32_t key[KPT];
-  bool special = false;
-  load_keys<T, VEC, KPT>(x, 0, N, key, special);
+  // The sample load goes first so that the bound waits for it alone while
+  // the row loads are still in flight.
   const uint32_t samp = sample_key(x, N);
+  uint32_t key[KPT];
+  issue_row_loads<T, VEC, KPT>(x, 0, N, key);
+  if (tid == 0) s_max = 0;
+  const uint32_t L = sample_bound(samp, K, N, hist, s_pick);  // has barriers
   MOE_PHASE(1);
-  rekey_if_special<KPT>(key, special);
+  bool special = false;
+  keys_from_bits<T, VEC, KPT>(x, 0, N, key, special);
+  rekey_if_special<KPT>(key, special);  // has a barrier
   uint32_t kmax = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) kmax = max(kmax, key[i]);
   kmax = wave_max_u32(kmax);
-  if (tid == 0) s_max = 0;
-  __syncthreads();
   if (lane == 0) atomicMax(&s_max, kmax);
-  const uint32_t L = sample_bound(samp, K, N, hist, s_pick);  // has barriers
   MOE_PHASE(2);
-  const uint32_t rmax = s_max;
 
   // ---- candidate mask: keys >= L, else exact mode ----
   uint32_t mask = 0;
@@ -721,30 +736,12 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
     base = st.prefix;
   }
   MOE_PHASE(3);
+  const uint32_t rmax = s_max;  // complete: the scans above hold barriers
 
-  // ---- extraction: candidate columns re-read from L2 ----
-  {
-    constexpr int BATCH = 4;  // loads in flight per lane
-    const uint32_t rounds = wave_max_u32((uint32_t)__popc(mask));
-    for (uint32_t it = 0; it < rounds; it += BATCH) {
-      int col[BATCH];
-      uint32_t bits[BATCH];
+  // ---- extraction from the key registers (fully unrolled, no indexing) ----
 #pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        col[u] = -1;
-        if (mask) {
-          const int i = __ffs(mask) - 1;
-          mask &= mask - 1;
-          col[u] = VEC * (tid + kRadixThreads * (i / VEC)) + (i % VEC);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u) bits[u] = Elem<T>::bits(x + (col[u] >= 0 ? col[u] : 0));
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u)
-        if (col[u] >= 0) cand[cpos++] = make_comp(key_of_bits(bits[u]), (uint32_t)col[u]);
-    }
-  }
+  for (int i = 0; i < KPT; ++i)
+    if ((mask >> i) & 1u) cand[cpos++] = make_comp(key[i], slot_col<VEC>(0, i));
   __syncthreads();
   MOE_PHASE(4);
   order_and_store(cand, (int)C, base, rmax, K, row, tmp, hist, bstart, wsum, &s_flag, s_red, scores, indices);
@@ -804,20 +801,20 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   const int end = min(N, c0 + slice);
 
   MOE_PHASE(0);
-  uint32_t key[KPT];
-  bool special = false;
-  load_keys<T, VEC, KPT>(x, c0, end, key, special);
   const uint32_t samp = sample_key(x, N);
+  uint32_t key[KPT];
+  issue_row_loads<T, VEC, KPT>(x, c0, end, key);
+  if (tid == 0) s_max = 0;
+  const uint32_t L = sample_bound(samp, K, N, hist, s_pick);  // has barriers
   MOE_PHASE(1);
-  rekey_if_special<KPT>(key, special);
+  bool special = false;
+  keys_from_bits<T, VEC, KPT>(x, c0, end, key, special);
+  rekey_if_special<KPT>(key, special);  // has a barrier
   uint32_t kmax = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) kmax = max(kmax, key[i]);
   kmax = wave_max_u32(kmax);
-  if (tid == 0) s_max = 0;
-  __syncthreads();
   if (lane == 0) atomicMax(&s_max, kmax);
-  const uint32_t L = sample_bound(samp, K, N, hist, s_pick);  // has barriers
   MOE_PHASE(2);
 
   uint32_t mask = 0;
@@ -832,32 +829,13 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   __syncthreads();
   cpos += s_base;
   MOE_PHASE(3);
-  {
-    constexpr int BATCH = 4;
-    const uint32_t rounds = wave_max_u32((uint32_t)__popc(mask));
-    for (uint32_t it = 0; it < rounds; it += BATCH) {
-      int col[BATCH];
-      uint32_t bits[BATCH];
 #pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        col[u] = -1;
-        if (mask) {
-          const int i = __ffs(mask) - 1;
-          mask &= mask - 1;
-          col[u] = c0 + VEC * (tid + kRadixThreads * (i / VEC)) + (i % VEC);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u) bits[u] = Elem<T>::bits(x + (col[u] >= 0 ? col[u] : 0));
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        if (col[u] >= 0) {
-          if (cpos < (uint32_t)kCandCap)
-            __hip_atomic_store(rcand + cpos, make_comp(key_of_bits(bits[u]), (uint32_t)col[u]),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ++cpos;
-        }
-      }
+  for (int i = 0; i < KPT; ++i) {
+    if ((mask >> i) & 1u) {
+      if (cpos < (uint32_t)kCandCap)
+        __hip_atomic_store(rcand + cpos, make_comp(key[i], slot_col<VEC>(c0, i)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      ++cpos;
     }
   }
   MOE_PHASE(4);
