@@ -140,6 +140,23 @@ def test_invalid_arguments_raise(cuda):
         K.grouped_gemm(X, W, torch.zeros(5, dtype=torch.int64, device=cuda))
 
 
+def test_large_tiles_ragged(cuda):
+    """Problems big enough for the largest tiles, with H not a multiple of
+    the k-tile, I not a multiple of the n-tile, one crowded expert and
+    invalid ids."""
+    T, topk, E, H, I = 8192, 2, 16, 1000, 1900
+    X, W = make(T, H, I, E, seed=21)
+    g = torch.Generator().manual_seed(21)
+    ids = torch.randint(0, E, (T, topk), generator=g)
+    ids[:2000, 0] = 3                                    # crowded expert
+    ids[::97, 1] = torch.randint(E, E + 5, (ids[::97, 1].numel(),), generator=g)  # invalid
+    Y = check_gemm(X, W, ids.to(cuda), topk)
+    bad = ((ids < 0) | (ids >= E)).flatten().to(cuda)
+    assert bad.any() and (Y[bad] == 0).all()
+    # all rows on one expert
+    check_gemm(X, W, torch.full((T, topk), 5, device=cuda), topk)
+
+
 def test_config4_fusedmoe_test_shape(cuda):
     """T=4096, H=1024, I=256, E=8, top-2 from topk of N(0,1) logits -> 8192 rows."""
     g = torch.Generator().manual_seed(0)

@@ -215,6 +215,27 @@ template <> struct MfmaOp<Half16> {  // float16
   }
 };
 
+// s_waitcnt vmcnt(N) with every other counter left alone (N <= 63).
+template <int N>
+__device__ inline void vm_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | 0x0F70);
+}
+
+template <int V> struct IntC { static constexpr int value = V; };
+
+// Calls fn(IntC<min(n, F)>) for a wave-uniform n >= 0: one specialised body
+// per value, chosen by scalar branches.
+template <int F, typename Fn>
+__device__ inline void with_count(int n, Fn&& fn) {
+  if constexpr (F == 0) {
+    fn(IntC<0>{});
+  } else {
+    if (n >= F) fn(IntC<F>{});
+    else with_count<F - 1>(n, fn);
+  }
+}
+
 // Tile configurations.  A workgroup computes a BM x BN tile of one expert
 // with WM x WN waves, each owning FM x FN blocks of 32x32 (v_mfma 32x32x16);
 // K advances BK elements per pipeline stage and STAGES stages are in LDS.
@@ -248,8 +269,9 @@ struct GemmCfg {
   static_assert(LDS_BYTES + BM * 4 <= 160 * 1024, "LDS budget");
   static __device__ inline int slot(int r, int c) { return r * CPR + (c ^ ((r / (8 / CPR)) % CPR)); }
 };
-using CfgLarge = GemmCfg<128, 256, 2, 2, 32, 2, 2>;  // 4 waves of 64x128, 48 KB LDS, 2 per CU
-using CfgSmall = GemmCfg<64, 128, 2, 2, 64, 3>;   // 4 waves of 32x64,    72 KB LDS
+using CfgHuge = GemmCfg<256, 256, 2, 4, 64, 2, 1>;   // 8 waves of 128x64, 128 KB LDS, 1 per CU
+using CfgLarge = GemmCfg<128, 256, 2, 2, 32, 2, 2>;  // 4 waves of 64x128,  48 KB LDS, 2 per CU
+using CfgSmall = GemmCfg<64, 128, 2, 2, 64, 3>;      // 4 waves of 32x64,   72 KB LDS
 
 template <typename T, typename Cfg, int MODE = 0>  // MODE: tuning builds only (1 = copies only, 2 = MFMA only)
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
@@ -260,7 +282,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
     const int32_t* __restrict__ meta) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, S = Cfg::STAGES, CPR = Cfg::CPR;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];  // [S][(BM+BN)*BK]
-  __shared__ int32_t srow[BM];
+  __shared__ __attribute__((aligned(16))) int32_t srow[BM];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -373,7 +395,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
   // MFMAs of the others are skipped, so a tile costs MFMA time in
   // proportion to its rows, rounded up to 32.
   const int mcount = min(BM, mend - m0);
-  const int fm_act = min(Cfg::FM, max(0, (mcount - wm * Cfg::FM * 32 + 31) / 32));
+  const int fm_act = __builtin_amdgcn_readfirstlane(min(Cfg::FM, max(0, (mcount - wm * Cfg::FM * 32 + 31) / 32)));
   f32x16 acc[Cfg::FM][Cfg::FN];
 #pragma unroll
   for (int i = 0; i < Cfg::FM; ++i)
@@ -385,71 +407,93 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
 #pragma unroll
   for (int p = 0; p < S - 1; ++p) issue(p);
 
-  for (int kt = 0; kt < nk; ++kt) {
-    // Wait for this thread's copies of k-tile kt (the younger tiles, up to
-    // S-2 of them, stay in flight), then make everyone's copies visible.
-    const int younger = min(S - 2, nk - 1 - kt) * (Cfg::A_INS + Cfg::B_INS);
-    switch (younger) {  // s_waitcnt needs an immediate; the counts are small
-#define MOE_VMWAIT(n) case n: __builtin_amdgcn_s_waitcnt(((n) & 0xF) | ((((n) >> 4) & 3) << 14) | 0x0F70); break;
-      MOE_VMWAIT(0) MOE_VMWAIT(4) MOE_VMWAIT(6) MOE_VMWAIT(8) MOE_VMWAIT(12) MOE_VMWAIT(16)
-      MOE_VMWAIT(18) MOE_VMWAIT(24) MOE_VMWAIT(30) MOE_VMWAIT(32) MOE_VMWAIT(36) MOE_VMWAIT(40)
-      MOE_VMWAIT(48) MOE_VMWAIT(54) MOE_VMWAIT(60)
-#undef MOE_VMWAIT
-      default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    }
-    // Plain s_barrier: __syncthreads() would also wait for the younger
-    // k-tiles still in flight (its release fence drains vmcnt).
-    __builtin_amdgcn_s_barrier();
-    // All waves finished k-tile kt-1, so its slot may be refilled.
-    issue(kt + S - 1);
-    const uint16_t* st = smem + (kt % S) * Cfg::STAGE_ELEMS;
-    if (ktail && kt == nk - 1) {
-      // Zero the chunks past H of the last k-tile in both operands.
-      uint16_t* sw = const_cast<uint16_t*>(st);
-      const int64_t k = (int64_t)kt * BK;
-      for (int q = tid; q < (BM + BN) * CPR; q += Cfg::THREADS) {
-        const int r = q / CPR, pos = q % CPR, c = pos ^ ((r / (8 / CPR)) % CPR);
-        if (k + c * 8 >= H) *reinterpret_cast<u32x4*>(sw + q * 8) = u32x4{0u, 0u, 0u, 0u};
+  // The k loop, specialised on the number FA of active 32-row blocks so
+  // that the skip is a scalar branch taken once per tile.  Per k-tile: wait
+  // for this thread's copies of the tile (the S-2 younger tiles stay in
+  // flight; the last tiles wait for all), barrier, refill the slot that
+  // k-tile kt-1 used, then BK/16 MFMA steps.  Operand fragments are double
+  // buffered in registers: the LDS reads of step s+1 are issued before the
+  // MFMAs of step s.
+  auto k_loop = [&](auto fa_tag) {
+    constexpr int FA = decltype(fa_tag)::value;
+    constexpr int FAR = FA > 0 ? FA : 1;
+    constexpr int STEPS = BK / 16;
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + S - 2 < nk) vm_wait<(S - 2) * (Cfg::A_INS + Cfg::B_INS)>();
+      else vm_wait<0>();
+      // Plain s_barrier: __syncthreads() would also wait for the younger
+      // k-tiles still in flight (its release fence drains vmcnt).
+      __builtin_amdgcn_s_barrier();
+      issue(kt + S - 1);
+      const uint16_t* st = smem + (kt % S) * Cfg::STAGE_ELEMS;
+      if (ktail && kt == nk - 1) {
+        // Zero the chunks past H of the last k-tile in both operands.
+        uint16_t* sw = const_cast<uint16_t*>(st);
+        const int64_t k = (int64_t)kt * BK;
+        for (int q = tid; q < (BM + BN) * CPR; q += Cfg::THREADS) {
+          const int r = q / CPR, pos = q % CPR, c = pos ^ ((r / (8 / CPR)) % CPR);
+          if (k + c * 8 >= H) *reinterpret_cast<u32x4*>(sw + q * 8) = u32x4{0u, 0u, 0u, 0u};
+        }
+        __syncthreads();
       }
-      __syncthreads();
-    }
-    const u32x4* As = reinterpret_cast<const u32x4*>(st);
-    const u32x4* Bs = reinterpret_cast<const u32x4*>(st + BM * BK);
+      const u32x4* As = reinterpret_cast<const u32x4*>(st);
+      const u32x4* Bs = reinterpret_cast<const u32x4*>(st + BM * BK);
+      u32x4 a[2][FAR], b[2][Cfg::FN];
+      auto load = [&](int s, int q) {
+        const int c = 2 * s + (lane >> 5);
 #pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      const int c = 2 * s + (lane >> 5);
-      u32x4 a[Cfg::FM], b[Cfg::FN];
+        for (int i = 0; i < FA; ++i) a[q][i] = As[Cfg::slot(wm * Cfg::FM * 32 + i * 32 + (lane & 31), c)];
 #pragma unroll
-      for (int i = 0; i < Cfg::FM; ++i)
-        if (i < fm_act) a[i] = As[Cfg::slot(wm * Cfg::FM * 32 + i * 32 + (lane & 31), c)];
+        for (int j = 0; j < Cfg::FN; ++j) b[q][j] = Bs[Cfg::slot(wn * Cfg::FN * 32 + j * 32 + (lane & 31), c)];
+      };
+      if constexpr (FA > 0 || MODE == 1) load(0, 0);
 #pragma unroll
-      for (int j = 0; j < Cfg::FN; ++j) b[j] = Bs[Cfg::slot(wn * Cfg::FN * 32 + j * 32 + (lane & 31), c)];
-      if (MODE == 1) {
-        acc[0][0][0] += __uint_as_float(a[0][0] ^ b[0][0]);
-        continue;
+      for (int s = 0; s < STEPS; ++s) {
+        if constexpr (FA > 0 || MODE == 1)
+          if (s + 1 < STEPS) load(s + 1, (s + 1) & 1);
+        if constexpr (MODE == 1) {
+          acc[0][0][0] += __uint_as_float(a[s & 1][0][0] ^ b[s & 1][0][0]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < FA; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FN; ++j) acc[i][j] = MfmaOp<T>::run(a[s & 1][i], b[s & 1][j], acc[i][j]);
+        }
       }
+      if constexpr (MODE != 1 && FA > 0) {
+        // Instruction order of the k-tile: step 0's LDS reads, then each
+        // step's MFMAs with the next step's reads placed one after each
+        // MFMA, so those reads are in flight while the MFMAs run.
+        __builtin_amdgcn_sched_group_barrier(0x100, FA + Cfg::FN, 0);
 #pragma unroll
-      for (int i = 0; i < Cfg::FM; ++i)
-        if (i < fm_act)
+        for (int s = 0; s < STEPS; ++s)
 #pragma unroll
-          for (int j = 0; j < Cfg::FN; ++j) acc[i][j] = MfmaOp<T>::run(a[i], b[j], acc[i][j]);
+          for (int m = 0; m < FA * Cfg::FN; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (s + 1 < STEPS && m < FA + Cfg::FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+      }
     }
-  }
+  };
+  with_count<Cfg::FM>(fm_act, k_loop);
 
   // Epilogue: accumulator v of lane l holds row 8*(v/4) + 4*(l/32) + v%4,
   // column l%32 of its 32x32 block.  Rows go back to their routed position.
 #pragma unroll
   for (int i = 0; i < Cfg::FM; ++i) {
     if (i >= fm_act) continue;
+    int sr[16];  // routed rows of this lane's 16 accumulator rows, 4 per LDS read
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int4 q = *reinterpret_cast<const int4*>(srow + (wm * Cfg::FM + i) * 32 + g * 8 + (lane >> 5) * 4);
+      sr[4 * g] = q.x; sr[4 * g + 1] = q.y; sr[4 * g + 2] = q.z; sr[4 * g + 3] = q.w;
+    }
 #pragma unroll
     for (int j = 0; j < Cfg::FN; ++j) {
       const int64_t col = n0 + (wn * Cfg::FN + j) * 32 + (lane & 31);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = (wm * Cfg::FM + i) * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        const int sr = srow[r];
-        if (sr >= 0 && col < I) Y[(int64_t)sr * I + col] = MfmaOp<T>::cvt(acc[i][j][v]);
-      }
+      for (int v = 0; v < 16; ++v)
+        if (sr[v] >= 0 && col < I) Y[(int64_t)sr[v] * I + col] = MfmaOp<T>::cvt(acc[i][j][v]);
     }
   }
   }  // tile loop
@@ -610,10 +654,13 @@ extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert
   int32_t* t_exp = reinterpret_cast<int32_t*>(ws + g.tile_expert);
   int32_t* t_ms = reinterpret_cast<int32_t*>(ws + g.tile_mstart);
   int32_t* meta = reinterpret_cast<int32_t*>(ws + g.meta);
-  // Large tiles when they still give every CU about two of them.
-  const bool large = ((R + CfgLarge::BM - 1) / CfgLarge::BM) * ((I + CfgLarge::BN - 1) / CfgLarge::BN) >= 512;
-  const int bm = large ? CfgLarge::BM : CfgSmall::BM;
-  const int bn = large ? CfgLarge::BN : CfgSmall::BN;
+  // The largest tiles that still give every CU about two of them: 256x256
+  // (BK 64, full 128-byte lines per row copy) moves the least data per
+  // MFMA; smaller problems take smaller tiles to fill the chip.
+  auto tiles_of = [&](int64_t bm, int64_t bn) { return ((R + bm - 1) / bm) * ((I + bn - 1) / bn); };
+  const int cfg = tiles_of(CfgHuge::BM, CfgHuge::BN) >= 512 ? 2 : tiles_of(CfgLarge::BM, CfgLarge::BN) >= 512 ? 1 : 0;
+  const int bm = cfg == 2 ? CfgHuge::BM : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
+  const int bn = cfg == 2 ? CfgHuge::BN : cfg == 1 ? CfgLarge::BN : CfgSmall::BN;
   int rc;
   if (idx_dtype == MOE_I64)
     rc = launch_route(static_cast<const int64_t*>(expert_ids), R, (int)E, blockcnt, counts, offsets, sorted,
@@ -626,13 +673,13 @@ extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert
   const uint16_t* x = static_cast<const uint16_t*>(X);
   const uint16_t* w = static_cast<const uint16_t*>(W);
   uint16_t* y = static_cast<uint16_t*>(Y);
-  if (large) {
-    if (dtype == MOE_BF16) rc = launch_gemm<uint16_t, CfgLarge>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
-    else rc = launch_gemm<Half16, CfgLarge>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
-  } else {
-    if (dtype == MOE_BF16) rc = launch_gemm<uint16_t, CfgSmall>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
-    else rc = launch_gemm<Half16, CfgSmall>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
-  }
+  auto run = [&](auto cfg_tag) {
+    using C = decltype(cfg_tag);
+    return dtype == MOE_BF16
+               ? launch_gemm<uint16_t, C>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta)
+               : launch_gemm<Half16, C>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
+  };
+  rc = cfg == 2 ? run(CfgHuge{}) : cfg == 1 ? run(CfgLarge{}) : run(CfgSmall{});
   if (rc) return rc;
   return check_launch("grouped_gemm_kernel");
 }
