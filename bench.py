@@ -9,7 +9,8 @@ by the measured time per call, in GB/s.
 
 The other BASELINE configurations are measured after the headline and
 reported under "secondary" (router C1/C3a/C3b in us and GB/s, grouped GEMM
-C4/C5 in TFLOP/s with %MFMA and %HBM).  ``cpu_baseline`` is the reference's
+C4/C5 in TFLOP/s with %MFMA and %HBM, the fused router GEMM + TopK +
+softmax on the reference's router-fusion models).  ``cpu_baseline`` is the reference's
 CPU PyTorch path (torch.topk + softmax, kernels/topk_softmax_baseline.py:39-66)
 timed on this host's cores on the same C2 input.
 
@@ -35,7 +36,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", default="", help="comma list of c1,c2,c3a,c3b,c4,c5 (profiling runs)")
+    p.add_argument("--only", default="", help="comma list of c1,c2,c3a,c3b,c4,c5,router (profiling runs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 1 GiB device-to-device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -211,6 +212,37 @@ def main():
     if want("c5"):
         gemm_cfg("c5", "grouped_gemm bf16 T=4096 H=7168 I=2048 E=256 top-8 skewed (32768 rows)",
                  4096, 7168, 2048, 256, 8, True)
+
+    # ---------------- fused router GEMM + TopK + softmax ----------------
+    # The reference's router-fusion benchmark models (benchmarks/benchmark_router_fusion.py:169-174)
+    # at 256 and 16384 tokens: fused kernel vs the two-launch path (router_gemm + topk_softmax)
+    # and torch (bf16 matmul + topk + softmax) on the same GPU.
+    fused_cfgs = {"r_qwen2_t256": ("Qwen2-57B", 256, 3584, 64, 8),
+                  "r_qwen3_t256": ("Qwen3-235B", 256, 4096, 128, 8),
+                  "r_dsv2_t256": ("DeepSeek-V2", 256, 5120, 160, 6),
+                  "r_dsv2_t16384": ("DeepSeek-V2", 16384, 5120, 160, 6)}
+    for name, (model, T, H, E, Kk) in fused_cfgs.items():
+        if not want(name) and not want("router"):
+            continue
+        gr = torch.Generator(device=dev).manual_seed(0)
+        X = torch.randn(T, H, generator=gr, device=dev).bfloat16()
+        W = torch.randn(H, E, generator=gr, device=dev).bfloat16()
+        K.router_topk_softmax(X, W, Kk)  # transposed weight cached before timing
+        us = graph_time_ms(lambda: K.router_topk_softmax(X, W, Kk)) * 1e3
+        us_two = graph_time_ms(lambda: K.topk_softmax(K.router_gemm(X, W), Kk)) * 1e3
+
+        def torch_router():
+            v, i = torch.topk(X @ W, Kk, dim=-1)
+            return torch.softmax(v.float(), dim=-1), i
+
+        us_torch = gpu_time_ms(torch_router, 50, 5) * 1e3
+        nb = T * H * 2 + H * E * 2 + T * Kk * 8
+        fl = 2.0 * T * H * E
+        secondary[name] = {"workload": f"fused router {model} T={T} H={H} E={E} K={Kk} bf16", "us": us,
+                           "us_two_launch": us_two, "us_torch": us_torch, "GB_s": nb / us / 1e3,
+                           "frac_hbm": nb / us / 1e3 / HBM_PEAK_GBS, "TFLOP_s": fl / us / 1e6,
+                           "timing": "us, us_two_launch: HIP-graph replay; us_torch: eager torch on the GPU"}
+        del X, W
 
     # ---------------- CPU baseline (reference torch path) ----------------
     cpu = None

@@ -152,6 +152,53 @@ int moe_grouped_gemm(const void* X, const void* W, const void* expert_ids,
                      int64_t I, int64_t E, void* Y, void* workspace,
                      size_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------------
+ * Router GEMM (logits = X . W) and the fused router GEMM + TopK + softmax.
+ * The weights are used transposed, Wt [E, H], so that both MFMA operands
+ * are K-contiguous; moe_router_weight_transpose builds Wt from the
+ * reference's W [H, E] (a caller keeps Wt while W is unchanged).
+ * ------------------------------------------------------------------- */
+
+/* Wt [E, H] = W [H, E]^T (dtype MOE_BF16 or MOE_F16; W rows ldw >= E
+ * elements apart, so a column-padded W [H, E_padded] is read in place).
+ * Replaces the per-call weight padding of the reference's router wrappers
+ * (_pad_W, kernels/router_gemm_topk_softmax.py:1160-1166): any E works, no
+ * power-of-two padding is needed. */
+int moe_router_weight_transpose(const void* W, int dtype, int64_t H, int64_t E,
+                                int64_t ldw, void* Wt, void* stream);
+
+/* Workspace bytes moe_router_gemm / moe_router_topk_softmax need for T
+ * tokens (split-H partial tiles when T is small; always >= 4096). */
+size_t moe_router_workspace_size(int64_t T, int64_t H, int64_t E);
+
+/* logits [T, E] fp32 = X [T, H] . Wt [E, H]^T, fp32 accumulation.
+ * Replaces router_gemm_kernel / get_router_gemm_kernel
+ * (kernels/router_gemm_topk_softmax.py:78-145), which writes fp32 logits
+ * of the padded width E_padded; here the output is exactly [T, E].
+ *   X, Wt   dtype MOE_BF16 or MOE_F16, 16-byte aligned; H a multiple of 8.
+ */
+int moe_router_gemm(const void* X, const void* Wt, int dtype, int64_t T,
+                    int64_t H, int64_t E, float* logits, void* workspace,
+                    size_t ws_bytes, void* stream);
+
+/* Fused router: per token, the K largest logits of X . Wt^T, their softmax
+ * (Convention B, as moe_topk_softmax) and their expert indices; the logits
+ * never leave LDS.
+ * Replaces the fused kernels returned by get_fused_router_kernel
+ * (kernels/router_gemm_topk_softmax.py:1169-1203: cpasync/tma/tma_auto x
+ * selection/bitonic, :148-1150).  Results equal
+ * moe_topk_softmax(moe_router_gemm(X, Wt)): indices bit-exact (ties to the
+ * lower expert index; the reference's fused kernels pick the higher one,
+ * :224-229), scores to fp32 rounding.
+ *   scores  [T, K] fp32; indices [T, K] idx_dtype MOE_I32 or MOE_I64.
+ *   Limits: E <= 256, K <= 32 (MOE_EUNSUP beyond: use moe_router_gemm and
+ *   moe_topk_softmax).
+ */
+int moe_router_topk_softmax(const void* X, const void* Wt, int dtype, int64_t T,
+                            int64_t H, int64_t E, int64_t K, float* scores,
+                            void* indices, int idx_dtype, void* workspace,
+                            size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -89,3 +89,36 @@ def test_python_api_rejects_cpu_tensors():
         grouped_gemm(torch.randn(4, 16).bfloat16(), torch.randn(2, 8, 16).bfloat16(), torch.zeros(4, dtype=torch.int64))
     with pytest.raises(ValueError):
         topk_softmax(torch.randn(4, 16, 2), 2)
+
+
+def test_router_gemm_host_checks():
+    L = _lib.lib()
+    nul = None
+    # workspace: control block alone for large T, plus split partials for small T
+    assert L.moe_router_workspace_size(16384, 5120, 160) == 4096
+    assert L.moe_router_workspace_size(256, 5120, 160) > 4096
+    # fused limits: E > 256 or K > 32 -> unsupported; K > E -> invalid
+    assert L.moe_router_topk_softmax(16, 16, 1, 4, 64, 300, 8, 16, 16, 3, 16, 1 << 20, nul) == _lib.MOE_EUNSUP
+    assert L.moe_router_topk_softmax(16, 16, 1, 4, 64, 64, 33, 16, 16, 3, 16, 1 << 20, nul) == _lib.MOE_EUNSUP
+    assert L.moe_router_topk_softmax(16, 16, 1, 4, 64, 8, 9, 16, 16, 3, 16, 1 << 20, nul) == _lib.MOE_EINVAL
+    # H not a multiple of 8, bad dtype, misaligned operand, small workspace
+    assert L.moe_router_gemm(16, 16, 1, 4, 12, 8, 16, 16, 1 << 20, nul) == _lib.MOE_EUNSUP
+    assert L.moe_router_gemm(16, 16, 0, 4, 16, 8, 16, 16, 1 << 20, nul) == _lib.MOE_EINVAL
+    assert L.moe_router_gemm(18, 16, 1, 4, 16, 8, 16, 16, 1 << 20, nul) == _lib.MOE_EINVAL
+    assert L.moe_router_gemm(16, 16, 1, 4, 16, 8, 16, 16, 8, nul) == _lib.MOE_EINVAL
+    # T == 0 is a no-op success; the transpose checks its stride
+    assert L.moe_router_gemm(nul, nul, 1, 0, 16, 8, nul, 16, 1 << 20, nul) == _lib.MOE_OK
+    assert L.moe_router_weight_transpose(16, 1, 16, 8, 4, 16, nul) == _lib.MOE_EINVAL
+
+
+def test_router_python_api_shapes_and_names():
+    import torch
+    from tilelang_moe_amd.kernels import router_gemm_topk_softmax as R
+
+    assert R._next_pow2(160) == 256 and R._next_pow2(64) == 64
+    with pytest.raises(ValueError, match="Unknown algorithm"):
+        R.get_fused_router_kernel("wgmma", 256, 4096, 128, 8)
+    with pytest.raises(ValueError, match="GPU only"):
+        R.router_topk_softmax(torch.randn(4, 16).bfloat16(), torch.randn(16, 8).bfloat16(), 2)
+    for algo in R.FUSED_ALGOS:
+        assert callable(getattr(R, f"fused_router_{algo}_kernel")(256, 4096, 160, 256, 8))

@@ -188,3 +188,39 @@ def test_torch_baseline_gemm_loop_matches_oracle():
     ids = torch.randint(-1, 6, (40,), generator=g)
     np.testing.assert_allclose(tb.grouped_gemm_loop(X, W, ids).numpy(), og.grouped_gemm(X.numpy(), W.numpy(), ids.numpy()),
                                rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# Router GEMM oracle
+# ---------------------------------------------------------------------------
+from oracle import router_gemm as org  # noqa: E402
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_router_gemm_oracle_vs_bruteforce(seed):
+    """Small exact-integer inputs: the logits are exact, so the fp64 matmul
+    must equal the triple loop, and the top-K must equal repeated scans
+    (integer logits tie often, so the lower-index rule is exercised)."""
+    rng = np.random.default_rng(seed)
+    X = rng.integers(-3, 4, size=(9, 13)).astype(np.float32)
+    W = rng.integers(-2, 3, size=(13, 11)).astype(np.float32)
+    lg = org.logits_fp64(X, W)
+    np.testing.assert_array_equal(lg, np.array(org.brute_logits(X.tolist(), W.tolist())))
+    for k in (1, 3, 11):
+        idx = org.topk_order(lg, k)
+        for t in range(lg.shape[0]):
+            assert idx[t].tolist() == org.brute_topk(lg[t].tolist(), k)
+
+
+def test_router_gemm_oracle_closed_forms():
+    rng = np.random.default_rng(5)
+    lg = rng.standard_normal((7, 20))
+    s, i = org.topk_softmax_fp64(lg, 20)  # K == E: full stable sort
+    np.testing.assert_array_equal(i, np.argsort(-lg, axis=1, kind="stable"))
+    np.testing.assert_allclose(s.sum(axis=1), 1.0, rtol=0, atol=1e-15)
+    np.testing.assert_allclose(org.softmax_at(lg, i[:, :4]), org.topk_softmax_fp64(lg, 4)[0], rtol=1e-15)
+    # Conv B softmax of the top-k equals the renormalised full softmax (Z cancels).
+    full = np.exp(lg - lg.max(1, keepdims=True))
+    full /= full.sum(1, keepdims=True)
+    top = np.take_along_axis(full, i[:, :4], 1)
+    np.testing.assert_allclose(top / top.sum(1, keepdims=True), org.topk_softmax_fp64(lg, 4)[0], rtol=1e-13)

@@ -3,7 +3,9 @@
 Mirrors the hot-path names of the reference's kernels/__init__.py
 (:11-22 TopK+softmax, :31-35 grouped GEMM): ``topk_softmax`` and
 ``grouped_gemm`` are the recommended entry points, the other names are the
-per-algorithm variants the reference also exports.  Every function runs a
+per-algorithm variants the reference also exports.  The router GEMM and
+the fused router GEMM + TopK + softmax (kernels/router_gemm_topk_softmax.py
+in the reference) live in the submodule of the same name.  Every function runs a
 hand-written gfx950 HIP kernel from libmoe_hip.so.
 """
 from .topk_softmax import (
@@ -19,6 +21,12 @@ from .topk_softmax import (
     topk_softmax_sonic,
 )
 from .grouped_gemm import grouped_gemm, grouped_gemm_best, route_sort
+from .router_gemm_topk_softmax import (
+    get_fused_router_kernel,
+    get_router_gemm_kernel,
+    router_gemm,
+    router_topk_softmax,
+)
 
 __all__ = [
     "topk_softmax",
@@ -34,4 +42,8 @@ __all__ = [
     "grouped_gemm",
     "grouped_gemm_best",
     "route_sort",
+    "router_gemm",
+    "router_topk_softmax",
+    "get_router_gemm_kernel",
+    "get_fused_router_kernel",
 ]
