@@ -54,6 +54,14 @@ enum moe_topk_algo {
   MOE_TOPK_RADIX = 2       /* multi-pass radix select, any N, K <= 16384   */
 };
 
+/* Score conventions (argument `score_mode` of moe_topk_softmax_ex).  The
+ * selected indices and their order are the same in every mode. */
+enum moe_score_mode {
+  MOE_SCORES_TOPK = 0,        /* Convention B: softmax over the K selected logits */
+  MOE_SCORES_ALL = 1,         /* Convention A: softmax over all N logits, read at the K */
+  MOE_SCORES_TOPK_RENORM = 2  /* Convention A + renormalisation: equal to B */
+};
+
 /* Error codes. */
 #define MOE_OK 0
 #define MOE_EINVAL (-1)   /* bad shape, dtype, pointer or alignment        */
@@ -101,6 +109,18 @@ int moe_topk_softmax(const void* logits, int logits_dtype, int64_t M, int64_t N,
                      int64_t ld, int64_t K, float* scores, void* indices,
                      int idx_dtype, int algo, void* workspace, size_t ws_bytes,
                      void* stream);
+
+/* moe_topk_softmax with a score convention.
+ * MOE_SCORES_ALL replaces topk_softmax_separate
+ * (kernels/topk_softmax_baseline.py:15-36: softmax over all experts, then
+ * top-K; here the order is by logit, which only refines the order of the
+ * rounded probabilities) with one extra pass over the rows;
+ * MOE_SCORES_TOPK_RENORM replaces topk_softmax_conv_a_renorm (:223-237),
+ * algebraically equal to Convention B, and computes exactly that. */
+int moe_topk_softmax_ex(const void* logits, int logits_dtype, int64_t M, int64_t N,
+                        int64_t ld, int64_t K, float* scores, void* indices,
+                        int idx_dtype, int algo, int score_mode, void* workspace,
+                        size_t ws_bytes, void* stream);
 
 /* Workspace bytes moe_route_sort needs for R routed rows over E experts. */
 size_t moe_route_sort_workspace_size(int64_t R, int64_t E);

@@ -22,7 +22,9 @@ Pinned by (tests/test_oracle.py):
     K == 1 (first argmax, score 1.0);
   * scores: fp64 softmax of the selected values, sum to 1, and the
     reference's convention identity (Conv A-renorm == Conv B,
-    tests/test_topk_softmax_conventions.py:58-69 of the reference).
+    tests/test_topk_softmax_conventions.py:58-69 of the reference);
+  * Convention A (topk_softmax_conv_a): torch CPU softmax-then-topk of the
+    reference baseline on tie-free rows, and all-N scores summing to 1.
 """
 from __future__ import annotations
 
@@ -73,6 +75,21 @@ def topk_softmax(logits: np.ndarray, k: int) -> Tuple[np.ndarray, np.ndarray]:
     idx = topk_order(x, k)
     vals = np.take_along_axis(x, idx, axis=1)
     return softmax64(vals), idx
+
+
+def topk_softmax_conv_a(logits: np.ndarray, k: int) -> Tuple[np.ndarray, np.ndarray]:
+    """Convention A (topk_softmax_separate, kernels/topk_softmax_baseline.py:15-36):
+    the same k indices as topk_softmax, scored by the float64 softmax over
+    the whole row.  A row holding NaN scores NaN (as torch.softmax)."""
+    x = np.asarray(logits, dtype=np.float32)
+    idx = topk_order(x, k)
+    xd = x.astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        m = np.max(np.where(np.isnan(xd), -np.inf, xd), axis=1, keepdims=True)
+        e = np.exp(xd - m)
+        p = np.take_along_axis(e, idx, 1) / e.sum(axis=1, keepdims=True)
+    p[np.isnan(x).any(axis=1)] = np.nan
+    return p, idx
 
 
 def tie_rows(logits: np.ndarray, k: int) -> np.ndarray:

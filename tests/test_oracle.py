@@ -224,3 +224,22 @@ def test_router_gemm_oracle_closed_forms():
     full /= full.sum(1, keepdims=True)
     top = np.take_along_axis(full, i[:, :4], 1)
     np.testing.assert_allclose(top / top.sum(1, keepdims=True), org.topk_softmax_fp64(lg, 4)[0], rtol=1e-13)
+
+
+def test_conv_a_oracle_vs_torch_separate():
+    """Convention A oracle == the reference baseline topk_softmax_separate
+    (torch CPU softmax then topk) on tie-free rows; with K == N the scores
+    are the whole softmax and sum to 1."""
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(50, 300, generator=g)
+    for k in (1, 6, 64):
+        s_t, i_t = tb.topk_softmax_separate(x, k)
+        s_o, i_o = orc.topk_softmax_conv_a(x.numpy(), k)
+        clean = ~orc.tie_rows(x.numpy(), k)
+        np.testing.assert_array_equal(i_o[clean], i_t.numpy()[clean])
+        np.testing.assert_allclose(s_o, s_t.double().numpy(), rtol=2e-6, atol=0)
+    s_all, _ = orc.topk_softmax_conv_a(x.numpy(), 300)
+    np.testing.assert_allclose(s_all.sum(1), 1.0, rtol=0, atol=1e-12)
+    xn = x.numpy().copy()
+    xn[3, 7] = np.nan
+    assert np.isnan(orc.topk_softmax_conv_a(xn, 4)[0][3]).all()

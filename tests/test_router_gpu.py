@@ -226,3 +226,56 @@ def test_config3_bf16_ties(cuda, seed):
         print(f"N={x.shape[1]} k={k}: tie rows {int(ties.sum())}, torch.topk(gpu) differs on "
               f"{int(diff.sum())} rows, all of them tie rows: {bool((diff <= ties).all())}")
         assert (diff <= ties).all()  # differences only on tie rows
+
+
+# ---------------------------------------------------------------------------
+# Score conventions (reference kernels/topk_softmax_baseline.py).
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n,k,algo", [(64, 6, "bitonic"), (256, 8, "selection"), (1000, 64, "selection"),
+                                      (4096, 100, "radix"), (32768, 2048, "radix"), (40000, 512, "radix")])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_convention_a_all_algorithms(cuda, n, k, algo, dtype):
+    """Convention A: same indices as Convention B, scores = the float64
+    softmax over the whole row read at them, within 1e-5 relative (fp32
+    running sums over up to 40000 terms)."""
+    g = torch.Generator(device="cpu").manual_seed(n + k)
+    x = torch.randn(9, n, generator=g).to(dtype)
+    x[0, :] = 0.5  # all equal: scores 1/n
+    x = x.to(cuda)
+    sa, ia = K.topk_softmax_scores(x, k, "A", algo)
+    sb, ib = K.topk_softmax_scores(x, k, "B", algo)
+    sr, ir = K.topk_softmax_scores(x, k, "A_renorm", algo)
+    torch.cuda.synchronize()
+    assert torch.equal(ia, ib) and torch.equal(ir, ib) and torch.equal(sr, sb)
+    s_o, i_o = orc.topk_softmax_conv_a(x.float().cpu().numpy(), k)
+    np.testing.assert_array_equal(ia.cpu().numpy(), i_o)
+    np.testing.assert_allclose(sa.cpu().double().numpy(), s_o, rtol=1e-5, atol=0)
+    # Convention A scores renormalised over the K are Convention B's.
+    torch.testing.assert_close(sa / sa.sum(-1, keepdim=True), sb, rtol=2e-5, atol=0)
+
+
+def test_convention_a_special_values(cuda):
+    x = torch.randn(4, 300)
+    x[0, 5] = float("nan")
+    x[1, :] = float("-inf")
+    x[1, 7] = 2.0
+    x[2, 9] = float("inf")
+    x = x.to(cuda)
+    s, i = K.topk_softmax_separate(x, 4)
+    s_o, i_o = orc.topk_softmax_conv_a(x.cpu().numpy(), 4)
+    np.testing.assert_array_equal(i.cpu().numpy(), i_o)
+    s = s.cpu().double().numpy()
+    assert np.isnan(s[0]).all()
+    np.testing.assert_allclose(s[1], s_o[1], rtol=1e-6)  # one finite value: 1, then zeros
+    assert np.isnan(s[2]).all() == np.isnan(s_o[2]).all()
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 32768, 2048), (3, 65536, 512), (40, 5000, 1000)])
+def test_radix_scores_bitwise_reproducible(cuda, m, n, k):
+    """Softmax normalisers are summed in rank order, so repeated calls give
+    identical bits whatever order the candidates reached threads in."""
+    x = torch.randn(m, n, generator=torch.Generator().manual_seed(n)).to(cuda)
+    s0, i0 = K.topk_softmax_radix(x, k)
+    for _ in range(5):
+        s, i = K.topk_softmax_radix(x, k)
+        assert torch.equal(i, i0) and torch.equal(s, s0)

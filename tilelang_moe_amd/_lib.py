@@ -17,6 +17,7 @@ from ._build import LIB_PATH
 MOE_F32, MOE_BF16, MOE_F16, MOE_I32, MOE_I64 = 0, 1, 2, 3, 4
 MOE_TOPK_AUTO, MOE_TOPK_BITONIC, MOE_TOPK_SELECTION, MOE_TOPK_RADIX = -1, 0, 1, 2
 MOE_OK, MOE_EINVAL, MOE_EUNSUP, MOE_EHIP = 0, -1, -2, -3
+MOE_SCORES_TOPK, MOE_SCORES_ALL, MOE_SCORES_TOPK_RENORM = 0, 1, 2
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -31,6 +32,8 @@ SIGNATURES = {
     "moe_topk_softmax_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int]),
     "moe_topk_softmax": (_c_int, [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr,
                                   _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
+    "moe_topk_softmax_ex": (_c_int, [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr,
+                                     _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
     "moe_route_sort_workspace_size": (_c_size, [_c_i64, _c_i64]),
     "moe_grouped_gemm_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "moe_route_sort": (_c_int, [_c_ptr, _c_int, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr,

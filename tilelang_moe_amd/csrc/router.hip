@@ -387,6 +387,26 @@ __device__ inline uint32_t sample_bound(uint32_t samp, int K, int N, uint32_t* h
   return max(ss.prefix, 1u);
 }
 
+// x * 2^48 rounded down, exactly, for x in [0, 1] (0 for NaN or x < 2^-48).
+__device__ inline uint64_t fixed48(float x) {
+  const uint32_t b = __float_as_uint(x);
+  const int e = (int)(b >> 23);                      // biased exponent (x >= 0)
+  const uint64_t m = (uint64_t)((b & 0x7FFFFFu) | 0x800000u);  // x = m 2^(e - 150)
+  const int sh = e - 102;                            // x 2^48 = m 2^sh, sh <= 25
+  if (e == 0 || e > 127) return 0;
+  return sh >= 0 ? m << sh : (sh > -24 ? m >> -sh : 0);
+}
+
+__device__ inline uint64_t wave_sum_u64(uint64_t v) {
+  v += xor_lanes_u64<1>(v);
+  v += xor_lanes_u64<2>(v);
+  v += xor_lanes_u64<4>(v);
+  v += xor_lanes_u64<8>(v);
+  v += xor_lanes_u64<16>(v);
+  v += xor_lanes_u64<32>(v);
+  return v;
+}
+
 // Orders the C candidates in cand[] (LDS, distinct composites, the K largest
 // among them are the row's winners), applies the softmax and stores row
 // `row`.  tmp needs kCandCap entries, hist and bstart kOrdBuckets + 1.
@@ -394,7 +414,7 @@ template <typename IdxT>
 __device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uint32_t rmax, int K,
                                        int64_t row, uint64_t* tmp, uint32_t* hist, uint32_t* bstart,
                                        uint32_t* wsum, uint32_t* s_flag, float* s_red,
-                                       float* scores, IdxT* indices) {
+                                       float* scores, IdxT* indices, uint64_t* s_sum64) {
   constexpr int CPT = kCandCap / kRadixThreads;  // candidates per thread, max
   constexpr int BPT = kOrdBuckets / kRadixThreads;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -448,7 +468,6 @@ __device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uin
   int rk[CPT];
   float ex[CPT];
   uint32_t ix[CPT];
-  float part = 0.0f;
 #pragma unroll
   for (int u = 0; u < CPT; ++u) {
     const int p = tid + kRadixThreads * u;
@@ -462,17 +481,37 @@ __device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uin
       rk[u] = r;
       ix[u] = comp_idx(v);
       ex[u] = expf(value_of_key(comp_key(v)) - vmax);
-      if (r < K) part += ex[u];
     }
   }
   MOE_PHASE(12);
-  part = wave_sum_f32(part);
-  if (lane == 0) s_red[tid / kWave] = part;
+  // The normaliser is summed exactly, in fixed point, so the scores are
+  // bitwise reproducible whatever (atomic) order the candidates reached
+  // threads in: every winner's exp lies in [0, 1] and is converted to
+  // round-down multiples of 2^-48 (error <= K 2^-48 relative to a sum >= 1)
+  // and added as uint64, which is associative.  A NaN exp (a NaN or +inf
+  // in the row) makes every score NaN, as in torch.softmax.
+  uint64_t qsum = 0;
+  bool nan = false;
+#pragma unroll
+  for (int u = 0; u < CPT; ++u)
+    if (rk[u] < K) {
+      qsum += fixed48(ex[u]);
+      nan |= ex[u] != ex[u];
+    }
+  qsum = wave_sum_u64(qsum);
+  if (lane == 0) s_sum64[tid / kWave] = __ballot(nan) ? ~0ull : qsum;
   __syncthreads();
   MOE_PHASE(13);
-  float sum = 0.0f;
+  uint64_t total = 0;
+  bool any_nan = false;
 #pragma unroll
-  for (int w = 0; w < kRadixThreads / kWave; ++w) sum += s_red[w];
+  for (int w = 0; w < kRadixThreads / kWave; ++w) {
+    const uint64_t q = s_sum64[w];
+    any_nan |= q == ~0ull;
+    total += q;
+  }
+  const float sum = any_nan ? __builtin_nanf("") : (float)((double)total * 0x1p-48);
+  (void)s_red;
 #pragma unroll
   for (int u = 0; u < CPT; ++u)
     if (rk[u] < K) store_out(scores, indices, row * K + rk[u], ex[u] / sum, ix[u]);
@@ -640,6 +679,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   __shared__ uint32_t wsum[kRadixThreads / kWave];
   __shared__ uint32_t s_pick[3];
   __shared__ uint32_t s_max, s_flag;
+  __shared__ uint64_t s_sum64[kRadixThreads / kWave];
   __shared__ float s_red[kRadixThreads / kWave];
 
   const int tid = threadIdx.x;
@@ -744,7 +784,8 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
     if ((mask >> i) & 1u) cand[cpos++] = make_comp(key[i], slot_col<VEC>(0, i));
   __syncthreads();
   MOE_PHASE(4);
-  order_and_store(cand, (int)C, base, rmax, K, row, tmp, hist, bstart, wsum, &s_flag, s_red, scores, indices);
+  order_and_store(cand, (int)C, base, rmax, K, row, tmp, hist, bstart, wsum, &s_flag, s_red, scores, indices,
+                  s_sum64);
   MOE_PHASE(5);
 }
 
@@ -786,6 +827,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   __shared__ uint32_t wsum[kRadixThreads / kWave];
   __shared__ uint32_t s_pick[3];
   __shared__ uint32_t s_max, s_flag, s_base, s_last;
+  __shared__ uint64_t s_sum64[kRadixThreads / kWave];
   __shared__ float s_red[kRadixThreads / kWave];
 
   const int tid = threadIdx.x;
@@ -870,7 +912,8 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
     cand[p] = __hip_atomic_load(rcand + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   MOE_PHASE(6);
-  order_and_store(cand, (int)C, L, rmax, K, row, tmp, hist, bstart, wsum, &s_flag, s_red, scores, indices);
+  order_and_store(cand, (int)C, L, rmax, K, row, tmp, hist, bstart, wsum, &s_flag, s_red, scores, indices,
+                  s_sum64);
   MOE_PHASE(7);
 }
 
@@ -949,6 +992,60 @@ static int launch_select(const T* x, int64_t M, int N, int64_t ld, int K, float*
   else if (epl <= 16) launch_select_e<T, IdxT, 16>(x, M, N, ld, K, s, id, st);
   else return fail(MOE_EUNSUP, "selection router supports N <= 1024");
   return check_launch("topk_select_kernel");
+}
+
+// ===========================================================================
+// 4. Convention-A scores: softmax over the whole row, read at the K winners.
+//    Replaces topk_softmax_separate (kernels/topk_softmax_baseline.py:15-36):
+//    scores = softmax(logits) then topk.  The winners (and their order) are
+//    those of the top-K kernels; this pass rewrites their scores as
+//    exp(x[idx] - m) / sum_j exp(x[j] - m) over all N columns, m the row
+//    maximum.  One wave per row keeps a running (maximum, sum) per lane over
+//    the row, merges the lanes, then rescales.  A row holding a NaN gets NaN
+//    scores (as torch.softmax).
+// ===========================================================================
+template <typename T, typename IdxT>
+__global__ __launch_bounds__(256) void topk_scores_all_kernel(const T* __restrict__ logits, int64_t M, int N,
+                                                              int64_t ld, int K, float* __restrict__ scores,
+                                                              const IdxT* __restrict__ indices) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= M) return;  // wave-uniform
+  const T* x = logits + row * ld;
+  float m = -__builtin_inff(), sum = 0.0f;
+  bool nan = false;
+  for (int c = lane; c < N; c += kWave) {
+    const float v = __uint_as_float(Elem<T>::bits(x + c));
+    nan |= v != v;
+    if (v > m) {
+      sum = sum * expf(m - v) + 1.0f;
+      m = v;
+    } else {
+      sum += expf(v - m);
+    }
+  }
+  // Merge the lanes' (m, sum); lanes that saw only -inf carry sum 0 at -inf.
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const float m2 = xor_lanes_f32(m, o), s2 = xor_lanes_f32(sum, o);
+    const float mm = fmaxf(m, m2);
+    sum = (m == -__builtin_inff() ? 0.0f : sum * expf(m - mm)) + (m2 == -__builtin_inff() ? 0.0f : s2 * expf(m2 - mm));
+    m = mm;
+  }
+  nan = __ballot(nan) != 0;
+  for (int j = lane; j < K; j += kWave) {
+    const float v = __uint_as_float(Elem<T>::bits(x + (int64_t)indices[row * K + j]));
+    scores[row * K + j] = nan ? __builtin_nanf("") : expf(v - m) / sum;
+  }
+}
+
+template <typename T, typename IdxT>
+static int launch_scores_all(const void* logits, int64_t M, int64_t N, int64_t ld, int64_t K, float* s,
+                             const void* idx, hipStream_t st) {
+  const int64_t grid = (M + 3) / 4;
+  topk_scores_all_kernel<T, IdxT><<<dim3((unsigned)grid), 256, 0, st>>>(
+      static_cast<const T*>(logits), M, (int)N, ld, (int)K, s, static_cast<const IdxT*>(idx));
+  return check_launch("topk_scores_all_kernel");
 }
 
 constexpr int kRadixRegMaxK = 8192;
@@ -1124,6 +1221,17 @@ extern "C" int moe_topk_softmax(const void* logits, int logits_dtype, int64_t M,
                                 int64_t ld, int64_t K, float* scores, void* indices,
                                 int idx_dtype, int algo, void* workspace, size_t ws_bytes,
                                 void* stream) {
+  return moe_topk_softmax_ex(logits, logits_dtype, M, N, ld, K, scores, indices, idx_dtype, algo,
+                             MOE_SCORES_TOPK, workspace, ws_bytes, stream);
+}
+
+extern "C" int moe_topk_softmax_ex(const void* logits, int logits_dtype, int64_t M, int64_t N,
+                                   int64_t ld, int64_t K, float* scores, void* indices,
+                                   int idx_dtype, int algo, int score_mode, void* workspace,
+                                   size_t ws_bytes, void* stream) {
+  if (score_mode != MOE_SCORES_TOPK && score_mode != MOE_SCORES_ALL && score_mode != MOE_SCORES_TOPK_RENORM)
+    return fail(MOE_EINVAL, "topk_softmax: unknown score mode");
+  if (score_mode == MOE_SCORES_ALL && !scores) return fail(MOE_EINVAL, "topk_softmax: score mode ALL needs scores");
   if (M < 0 || N < 1 || K < 1 || K > N)
     return fail(MOE_EINVAL, "topk_softmax: need M >= 0, N >= 1 and 1 <= K <= N (got M=" +
                                 std::to_string(M) + ", N=" + std::to_string(N) +
@@ -1144,16 +1252,29 @@ extern "C" int moe_topk_softmax(const void* logits, int logits_dtype, int64_t M,
   if (M == 0) return MOE_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool i64 = idx_dtype == MOE_I64;
+  int rc;
   switch (logits_dtype) {
     case MOE_F32:
-      return i64 ? dispatch_topk<float, int64_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st)
-                 : dispatch_topk<float, int32_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st);
+      rc = i64 ? dispatch_topk<float, int64_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st)
+               : dispatch_topk<float, int32_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st);
+      if (rc == MOE_OK && score_mode == MOE_SCORES_ALL)
+        rc = i64 ? launch_scores_all<float, int64_t>(logits, M, N, ld, K, scores, indices, st)
+                 : launch_scores_all<float, int32_t>(logits, M, N, ld, K, scores, indices, st);
+      return rc;
     case MOE_BF16:
-      return i64 ? dispatch_topk<uint16_t, int64_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st)
-                 : dispatch_topk<uint16_t, int32_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st);
+      rc = i64 ? dispatch_topk<uint16_t, int64_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st)
+               : dispatch_topk<uint16_t, int32_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st);
+      if (rc == MOE_OK && score_mode == MOE_SCORES_ALL)
+        rc = i64 ? launch_scores_all<uint16_t, int64_t>(logits, M, N, ld, K, scores, indices, st)
+                 : launch_scores_all<uint16_t, int32_t>(logits, M, N, ld, K, scores, indices, st);
+      return rc;
     case MOE_F16:
-      return i64 ? dispatch_topk<Half16, int64_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st)
-                 : dispatch_topk<Half16, int32_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st);
+      rc = i64 ? dispatch_topk<Half16, int64_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st)
+               : dispatch_topk<Half16, int32_t>(logits, M, N, ld, K, scores, indices, algo, workspace, ws_bytes, st);
+      if (rc == MOE_OK && score_mode == MOE_SCORES_ALL)
+        rc = i64 ? launch_scores_all<Half16, int64_t>(logits, M, N, ld, K, scores, indices, st)
+                 : launch_scores_all<Half16, int32_t>(logits, M, N, ld, K, scores, indices, st);
+      return rc;
     default:
       return fail(MOE_EINVAL, "topk_softmax: logits must be float32, bfloat16 or float16");
   }

@@ -15,9 +15,14 @@ from .topk_softmax import (
     topk_softmax,
     topk_softmax_best,
     topk_softmax_bitonic,
+    topk_softmax_conv_a_renorm,
+    topk_softmax_conv_b_unfused,
+    topk_softmax_fused,
     topk_softmax_int64,
     topk_softmax_radix,
+    topk_softmax_scores,
     topk_softmax_selection,
+    topk_softmax_separate,
     topk_softmax_sonic,
 )
 from .grouped_gemm import grouped_gemm, grouped_gemm_best, route_sort
@@ -36,6 +41,11 @@ __all__ = [
     "topk_softmax_sonic",
     "topk_softmax_radix",
     "topk_softmax_int64",
+    "topk_softmax_fused",
+    "topk_softmax_conv_b_unfused",
+    "topk_softmax_separate",
+    "topk_softmax_conv_a_renorm",
+    "topk_softmax_scores",
     "topk_radix",
     "topk_radix_tilelang",
     "select_strategy",

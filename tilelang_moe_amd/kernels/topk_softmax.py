@@ -62,7 +62,7 @@ def _check_logits(logits: torch.Tensor, k) -> Tuple[torch.Tensor, int]:
 
 
 def _run(logits: torch.Tensor, k: int, algo: int, with_scores: bool,
-         index_dtype: torch.dtype = torch.int32):
+         index_dtype: torch.dtype = torch.int32, score_mode: int = _lib.MOE_SCORES_TOPK):
     logits, k = _check_logits(logits, k)
     m, n = logits.shape
     dev = logits.device
@@ -74,10 +74,10 @@ def _run(logits: torch.Tensor, k: int, algo: int, with_scores: bool,
     stream = _lib.current_stream(dev)
     ws_bytes = L.moe_topk_softmax_workspace_size(m, n, k, algo)
     ws = _lib.workspace(dev, stream, ws_bytes)
-    _lib.check(L.moe_topk_softmax(
+    _lib.check(L.moe_topk_softmax_ex(
         logits.data_ptr(), _LOGIT_DTYPES[logits.dtype], m, n, logits.stride(0), k,
         scores.data_ptr() if with_scores else None, indices.data_ptr(), _IDX_DTYPES[index_dtype],
-        algo, ws.data_ptr() if ws is not None else None, ws_bytes, stream))
+        algo, score_mode, ws.data_ptr() if ws is not None else None, ws_bytes, stream))
     return scores, indices
 
 
@@ -135,3 +135,44 @@ def topk_softmax_int64(logits: torch.Tensor, k: int, algo: str = "auto"
     """Same as ``topk_softmax`` with int64 indices (the dtype torch.topk and the
     reference baseline return); ``algo`` forces one of auto/bitonic/selection/radix."""
     return _run(logits, k, _ALGOS[algo], True, torch.int64)
+
+
+# ---------------------------------------------------------------------------
+# Score conventions of the reference's baselines (kernels/topk_softmax_baseline.py).
+# Every variant selects the same experts in the same order (value
+# descending, ties to the lower index); they differ in the normaliser.
+# ---------------------------------------------------------------------------
+def topk_softmax_fused(logits: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Convention B: softmax over the k selected logits (reference
+    topk_softmax_fused, :39-66).  Same as ``topk_softmax``."""
+    return _run(logits, k, _lib.MOE_TOPK_AUTO, True)
+
+
+topk_softmax_conv_b_unfused = topk_softmax_fused
+
+
+def topk_softmax_separate(logits: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Convention A: softmax over all experts, read at the top-k (reference
+    topk_softmax_separate, :15-36, softmax then torch.topk).  The top-k are
+    chosen by logit, the order the rounded probabilities refine only on
+    exact ties."""
+    return _run(logits, k, _lib.MOE_TOPK_AUTO, True, score_mode=_lib.MOE_SCORES_ALL)
+
+
+def topk_softmax_conv_a_renorm(logits: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Convention A + renormalisation (reference topk_softmax_conv_a_renorm,
+    :223-237): softmax over all experts, top-k, divided by their sum, which
+    equals Convention B algebraically and is computed as such."""
+    return _run(logits, k, _lib.MOE_TOPK_AUTO, True, score_mode=_lib.MOE_SCORES_TOPK_RENORM)
+
+
+def topk_softmax_scores(logits: torch.Tensor, k: int, convention: str = "B", algo: str = "auto",
+                        index_dtype: torch.dtype = torch.int32) -> Tuple[torch.Tensor, torch.Tensor]:
+    """TopK+softmax with an explicit score convention ("A", "A_renorm" or
+    "B") and algorithm (auto/bitonic/selection/radix)."""
+    modes = {"B": _lib.MOE_SCORES_TOPK, "A": _lib.MOE_SCORES_ALL, "A_renorm": _lib.MOE_SCORES_TOPK_RENORM}
+    if convention not in modes:
+        raise ValueError(f"convention must be one of {list(modes)}, got {convention!r}")
+    if index_dtype not in _IDX_DTYPES:
+        raise ValueError("index_dtype must be torch.int32 or torch.int64")
+    return _run(logits, k, _ALGOS[algo], True, index_dtype, modes[convention])
