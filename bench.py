@@ -36,7 +36,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", default="", help="comma list of c1,c2,c3a,c3b,c4,c5,router (profiling runs)")
+    p.add_argument("--only", default="", help="comma list of c1,c2,c3a,c3b,c4,c5,router,moe (profiling runs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 1 GiB device-to-device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -243,6 +243,31 @@ def main():
                            "frac_hbm": nb / us / 1e3 / HBM_PEAK_GBS, "TFLOP_s": fl / us / 1e6,
                            "timing": "us, us_two_launch: HIP-graph replay; us_torch: eager torch on the GPU"}
         del X, W
+
+    # ---------------- FusedMoE (routed + shared experts) ----------------
+    # The reference's FusedMoE benchmark configs (benchmarks/benchmark_fusedmoe.py:29-50),
+    # inputs as its generate_fusedmoe_inputs (randn / sqrt(fan_in)), bf16.
+    moe_cfgs = {"moe_small": ("Small-Test", 1024, 2048, 512, 8, 1, 2),
+                "moe_dsv3": ("DeepSeek-V3", 8192, 7168, 2048, 8, 1, 4)}
+    for name, (model, T, Dh, De, E, NS, Kk) in moe_cfgs.items():
+        if not want(name) and not want("moe"):
+            continue
+        gm = torch.Generator(device=dev).manual_seed(42)
+        rn = lambda *shape: (torch.randn(*shape, generator=gm, device=dev) / shape[-1] ** 0.5).bfloat16()  # noqa: E731
+        Ds = De * NS
+        x = torch.randn(T, Dh, generator=gm, device=dev).bfloat16()
+        mw = dict(router_weight=rn(E, Dh), shared_gate=rn(Ds, Dh), shared_up=rn(Ds, Dh), shared_down=rn(Dh, Ds),
+                  routed_gate=rn(E, De, Dh), routed_up=rn(E, De, Dh), routed_down=rn(E, Dh, De))
+        ms = graph_time_ms(lambda: K.fused_moe_routed(x, **mw, n_experts_per_token=Kk), calls=3, replays=5)
+        from oracle import torch_baseline as tb
+        ms_torch = gpu_time_ms(lambda: tb.fusedmoe_torch(x, *mw.values(), Kk), 5, 2)
+        flops = 2.0 * 3 * (T * Kk * Dh * De + T * Dh * Ds) + 2.0 * T * Dh * E
+        tf = flops / ms / 1e9
+        secondary[name] = {"workload": f"FusedMoE {model} T={T} H={Dh} I={De} E={E} shared={NS} top-{Kk} bf16",
+                           "ms": ms, "ms_torch": ms_torch, "TFLOP_s": tf, "frac_mfma": tf / BF16_PEAK_TFLOPS,
+                           "timing": "ms: HIP-graph replay of the whole forward; ms_torch: eager torch "
+                                     "fusedmoe_pytorch restatement on the GPU"}
+        del x, mw
 
     # ---------------- CPU baseline (reference torch path) ----------------
     cpu = None

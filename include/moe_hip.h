@@ -219,6 +219,52 @@ int moe_router_topk_softmax(const void* X, const void* Wt, int dtype, int64_t T,
                             void* indices, int idx_dtype, void* workspace,
                             size_t ws_bytes, void* stream);
 
+/* Grouped GEMM with the SwiGLU epilogue:
+ *   Y[r, :] = silu(X[r/topk] Wg[e]^T) * (X[r/topk] Wu[e]^T),  e = expert_ids[r]
+ * one kernel, fp32 accumulation, output in the input dtype.  Replaces step 1
+ * of the reference's routed-expert kernel (kernels/fusedmoe_tilelang.py:147-203:
+ * gate and up GEMMs, SiLU(gate) * up, stored as up_logits) and its shared-
+ * expert counterpart (:39-121).  Same arguments and workspace as
+ * moe_grouped_gemm with Wg, Wu [E, I, H]; rows with an id outside [0, E)
+ * are zero. */
+int moe_grouped_gemm_swiglu(const void* X, const void* Wg, const void* Wu,
+                            const void* expert_ids, int dtype, int idx_dtype,
+                            int64_t T, int64_t topk, int64_t H, int64_t I,
+                            int64_t E, void* Y, void* workspace, size_t ws_bytes,
+                            void* stream);
+
+/* out[t, :] = S[t, :] + sum_j w[t, j] * Yr[t*k + j, :]   (S may be NULL)
+ * fp32 sums in a fixed order (deterministic), output in dtype.  Replaces the
+ * weighting and scatter_reduce combine of the reference's routed experts
+ * (kernels/fusedmoe_tilelang.py:227-229, :413-423).
+ *   Yr [T*k, D], S [T, D], out [T, D] dtype MOE_BF16/F16; w [T, k] fp32. */
+int moe_combine(const void* Yr, const void* S, const float* w, int dtype, int64_t T,
+                int64_t k, int64_t D, void* out, void* stream);
+
+/* Workspace bytes of moe_fused_moe (control block, scratch, intermediates). */
+size_t moe_fused_moe_workspace_size(int64_t T, int64_t Dh, int64_t De, int64_t Ds,
+                                    int64_t E, int64_t k);
+
+/* Routed-expert FFN with a shared expert: out [T, Dh] for x [T, Dh].
+ * Replaces FusedMoETileLang.forward / fusedmoe_best
+ * (kernels/fusedmoe_tilelang.py:309-425, :654-690) with the semantics of
+ * fusedmoe_pytorch (kernels/fusedmoe_baseline.py:41-168): router logits
+ * x . router_w^T, Convention-A softmax top-k (softmax over all E, then the k
+ * largest), routed experts silu(x Wg^T) * (x Wu^T) . Wd^T weighted by their
+ * scores, plus the shared expert on every token.  The router works in fp32
+ * (the reference rounds its logits and softmax to the input dtype).
+ *   router_w [E, Dh]; shared_gate, shared_up [Ds, Dh]; shared_down [Dh, Ds]
+ *   (Ds = 0: no shared expert); routed_gate, routed_up [E, De, Dh];
+ *   routed_down [E, Dh, De]; all dtype, 16-byte aligned; Dh, De, Ds
+ *   multiples of 8.  topk_weights [T, k] fp32 and topk_ids [T, k] int32
+ *   receive the routing when not NULL. */
+int moe_fused_moe(const void* x, const void* router_w, const void* shared_gate,
+                  const void* shared_up, const void* shared_down, const void* routed_gate,
+                  const void* routed_up, const void* routed_down, int dtype, int64_t T,
+                  int64_t Dh, int64_t De, int64_t Ds, int64_t E, int64_t k, void* out,
+                  float* topk_weights, void* topk_ids, void* workspace, size_t ws_bytes,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

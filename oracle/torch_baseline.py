@@ -39,3 +39,32 @@ def grouped_gemm_loop(X: torch.Tensor, W: torch.Tensor, expert_indices: torch.Te
             continue
         Y[mask] = X[mask] @ W[e].T
     return Y
+
+
+def fusedmoe_torch(x, router_weight, shared_gate, shared_up, shared_down, routed_gate, routed_up, routed_down,
+                   k: int):
+    """The reference's fusedmoe_pytorch (kernels/fusedmoe_baseline.py:41-168) on
+    flat tokens x [T, Dh], restated: torch matmuls in the input dtype, a
+    per-expert loop and scatter_reduce.  Used as the torch GPU baseline."""
+    logits = x @ router_weight.T
+    scores = F.softmax(logits, dim=-1)
+    w, ids = torch.topk(scores, k, dim=-1, sorted=False)
+
+    def ffn(t, g, u, d):
+        return (F.silu(t @ g.T) * (t @ u.T)) @ d.T
+
+    out = ffn(x, shared_gate, shared_up, shared_down)
+    flat, fw = ids.view(-1), w.view(-1, 1)
+    order = flat.argsort()
+    counts = flat.bincount(minlength=routed_gate.shape[0]).cpu().tolist()
+    tok = order // k
+    cache = torch.zeros_like(x)
+    start = 0
+    for e, c in enumerate(counts):
+        if c == 0:
+            continue
+        rows = tok[start:start + c]
+        y = ffn(x[rows], routed_gate[e], routed_up[e], routed_down[e]) * fw[order[start:start + c]]
+        cache.scatter_reduce_(0, rows.view(-1, 1).expand(-1, x.shape[1]), y, reduce="sum")
+        start += c
+    return out + cache

@@ -243,3 +243,33 @@ def test_conv_a_oracle_vs_torch_separate():
     xn = x.numpy().copy()
     xn[3, 7] = np.nan
     assert np.isnan(orc.topk_softmax_conv_a(xn, 4)[0][3]).all()
+
+
+# ---------------------------------------------------------------------------
+# FusedMoE oracle
+# ---------------------------------------------------------------------------
+from oracle import fusedmoe as ofm  # noqa: E402
+
+
+def _moe_inputs(T, Dh, De, Ds, E, seed=0):
+    rng = np.random.default_rng(seed)
+    r = lambda *s: rng.standard_normal(s) / np.sqrt(s[-1])  # noqa: E731
+    return (r(T, Dh), r(E, Dh), r(Ds, Dh), r(Ds, Dh), r(Dh, Ds), r(E, De, Dh), r(E, De, Dh), r(E, Dh, De))
+
+
+def test_fusedmoe_oracle_closed_forms():
+    x, rw, sg, su, sd, rg, ru, rd = _moe_inputs(7, 16, 8, 8, 3)
+    # One expert, k = 1: the dense SwiGLU FFN (weight 1), plus the shared part.
+    out = ofm.fusedmoe(x, rw[:1], sg, su, sd, rg[:1], ru[:1], rd[:1], 1)
+    np.testing.assert_allclose(out, ofm.expert(x, sg, su, sd) + ofm.expert(x, rg[0], ru[0], rd[0]), rtol=1e-12)
+    # Zero router weights, k = E: every expert with weight 1/E; no shared expert.
+    out = ofm.fusedmoe(x, np.zeros_like(rw), None, None, None, rg, ru, rd, 3)
+    avg = sum(ofm.expert(x, rg[e], ru[e], rd[e]) for e in range(3)) / 3
+    np.testing.assert_allclose(out, avg, rtol=1e-12)
+    # Routing equals Convention A of oracle.router on the same logits.
+    w, ids = ofm.route(x, rw, 2)
+    s_o, i_o = orc.topk_softmax_conv_a((x @ rw.T).astype(np.float32), 2)
+    np.testing.assert_array_equal(ids, i_o)
+    np.testing.assert_allclose(w, s_o, rtol=1e-6)
+    # silu against its definition at a few points.
+    np.testing.assert_allclose(ofm.silu(np.array([0.0, 1.0, -2.0])), [0.0, 1 / (1 + np.exp(-1)), -2 / (1 + np.exp(2))])

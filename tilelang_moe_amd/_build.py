@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(REPO_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libmoe_hip.so")
 
-SOURCES = ["router.hip", "gemm.hip", "router_gemm.hip", "capi.cpp"]
+SOURCES = ["router.hip", "gemm.hip", "router_gemm.hip", "moe.hip", "capi.cpp"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32.

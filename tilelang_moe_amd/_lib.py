@@ -40,6 +40,13 @@ SIGNATURES = {
                                 _c_size, _c_ptr]),
     "moe_grouped_gemm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_i64, _c_i64, _c_i64,
                                   _c_i64, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "moe_grouped_gemm_swiglu": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_i64, _c_i64,
+                                         _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "moe_combine": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
+    "moe_fused_moe_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "moe_fused_moe": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64,
+                               _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_size,
+                               _c_ptr]),
     "moe_router_weight_transpose": (_c_int, [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "moe_router_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "moe_router_gemm": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr,

@@ -20,6 +20,7 @@
 #include "mfma_tile.h"
 
 #include <algorithm>
+#include <string>
 
 namespace moe {
 
@@ -187,14 +188,21 @@ using CfgHuge = GemmCfg<256, 256, 2, 4, 64, 2, 1>;   // 8 waves of 128x64, 128 K
 using CfgLarge = GemmCfg<128, 256, 2, 2, 32, 2, 2>;  // 4 waves of 64x128,  48 KB LDS, 2 per CU
 using CfgSmall = GemmCfg<64, 128, 2, 2, 64, 3>;      // 4 waves of 32x64,   72 KB LDS
 
-template <typename T, typename Cfg, int MODE = 0>  // MODE: tuning builds only (1 = copies only, 2 = MFMA only)
+// EPI 0: Y = X W^T.  EPI 1 (SwiGLU): Y = silu(X Wg^T) * (X Wu^T) with W = Wg and
+// W2 = Wu, both [E, I, H]; a tile then covers BN/2 output columns, its even
+// 32-column blocks holding gate rows and its odd blocks the up rows of the
+// same output columns, so a lane holds both factors of each output element.
+template <typename T, typename Cfg, int MODE = 0, int EPI = 0>  // MODE: tuning builds only (1 = copies only, 2 = MFMA only)
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
-    const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, uint16_t* __restrict__ Y,
+    const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
+    uint16_t* __restrict__ Y,
     int64_t H, int64_t I, int topk, int64_t R, int E, int ntn,
     const int32_t* __restrict__ sorted_rows, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_mstart,
     const int32_t* __restrict__ meta) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, S = Cfg::STAGES, CPR = Cfg::CPR;
+  constexpr int OBN = EPI == 1 ? BN / 2 : BN;  // output columns per tile
+  static_assert(EPI == 0 || Cfg::FN % 2 == 0, "SwiGLU pairs 32-column blocks within a wave");
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];  // [S][(BM+BN)*BK]
   __shared__ __attribute__((aligned(16))) int32_t srow[BM];
 
@@ -240,10 +248,10 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
   if (w >= n_super_items) {
     const int z = w - n_super_items;
     const int64_t z0 = (int64_t)offsets[E] + (int64_t)(z / ntn) * BM;
-    const int n0z = (z % ntn) * BN;
-    for (int i = tid; i < BM * BN; i += Cfg::THREADS) {
-      const int64_t p = z0 + i / BN;
-      const int64_t col = n0z + i % BN;
+    const int n0z = (z % ntn) * OBN;
+    for (int i = tid; i < BM * OBN; i += Cfg::THREADS) {
+      const int64_t p = z0 + i / OBN;
+      const int64_t col = n0z + i % OBN;
       if (p < R && col < I) Y[(int64_t)sorted_rows[p] * I + col] = 0;
     }
     continue;
@@ -258,7 +266,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
     nt = w % ntn;
   }
   if (mt >= n_tiles || nt >= ntn) continue;
-  const int n0 = nt * BN;
+  const int n0 = nt * OBN;  // first output column of the tile
 
   const int e = tile_expert[mt];
   const int m0 = tile_mstart[mt];
@@ -281,8 +289,15 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
   }
 #pragma unroll
   for (int i = 0; i < Cfg::B_INS; ++i) {
-    const int64_t n = n0 + Cfg::RPI * (wave * Cfg::B_INS + i) + crow;
-    b_src[i] = W + ((int64_t)e * I + (n < I ? n : 0)) * H + cchunk * 8;
+    const int nl = Cfg::RPI * (wave * Cfg::B_INS + i) + crow;  // tile row
+    if constexpr (EPI == 0) {
+      const int64_t n = n0 + nl;
+      b_src[i] = W + ((int64_t)e * I + (n < I ? n : 0)) * H + cchunk * 8;
+    } else {
+      const int blk = nl / 32;
+      const int64_t n = n0 + (blk >> 1) * 32 + (nl & 31);
+      b_src[i] = ((blk & 1) ? W2 : W) + ((int64_t)e * I + (n < I ? n : 0)) * H + cchunk * 8;
+    }
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   // 32-row blocks of this wave that hold routed rows (wave-uniform): the
@@ -311,12 +326,25 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
       const int4 q = *reinterpret_cast<const int4*>(srow + (wm * Cfg::FM + i) * 32 + g * 8 + (lane >> 5) * 4);
       sr[4 * g] = q.x; sr[4 * g + 1] = q.y; sr[4 * g + 2] = q.z; sr[4 * g + 3] = q.w;
     }
+    if constexpr (EPI == 0) {
 #pragma unroll
-    for (int j = 0; j < Cfg::FN; ++j) {
-      const int64_t col = n0 + (wn * Cfg::FN + j) * 32 + (lane & 31);
+      for (int j = 0; j < Cfg::FN; ++j) {
+        const int64_t col = n0 + (wn * Cfg::FN + j) * 32 + (lane & 31);
 #pragma unroll
-      for (int v = 0; v < 16; ++v)
-        if (sr[v] >= 0 && col < I) Y[(int64_t)sr[v] * I + col] = MfmaOp<T>::cvt(acc[i][j][v]);
+        for (int v = 0; v < 16; ++v)
+          if (sr[v] >= 0 && col < I) Y[(int64_t)sr[v] * I + col] = MfmaOp<T>::cvt(acc[i][j][v]);
+      }
+    } else {
+      // Blocks 2m (gate) and 2m+1 (up) of the tile hold output block m.
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; j += 2) {
+        const int64_t col = n0 + ((wn * Cfg::FN + j) >> 1) * 32 + (lane & 31);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float g = acc[i][j][v], u = acc[i][j + 1][v];
+          if (sr[v] >= 0 && col < I) Y[(int64_t)sr[v] * I + col] = MfmaOp<T>::cvt(g / (1.0f + expf(-g)) * u);
+        }
+      }
     }
   }
   }  // tile loop
@@ -390,13 +418,13 @@ static int launch_route(const IdxT* ids, int64_t R, int E, int32_t* blockcnt, in
   return check_launch("route_scatter_kernel");
 }
 
-template <typename T, typename Cfg, int MODE = 0>
-static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t H,
-                       int64_t I, int topk, int64_t R, int E, int ntn, const int32_t* sorted,
+template <typename T, typename Cfg, int MODE = 0, int EPI = 0>
+static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, const uint16_t* w2, uint16_t* y,
+                       int64_t H, int64_t I, int topk, int64_t R, int E, int ntn, const int32_t* sorted,
                        const int32_t* offsets, const int32_t* t_exp, const int32_t* t_ms, const int32_t* meta) {
   static bool attr_set = false;
   if (!attr_set) {
-    MOE_HIP_CHECK(hipFuncSetAttribute((const void*)grouped_gemm_kernel<T, Cfg, MODE>,
+    MOE_HIP_CHECK(hipFuncSetAttribute((const void*)grouped_gemm_kernel<T, Cfg, MODE, EPI>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cfg::LDS_BYTES));
     attr_set = true;
   }
@@ -404,8 +432,8 @@ static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, uin
   // the tile list can be long; otherwise one workgroup per possible tile.
   const int64_t ub = ((R + Cfg::BM - 1) / Cfg::BM + E + 1) * ntn;  // tiles, upper bound
   const int64_t grid = ub >= 16 * Cfg::SUPER ? 8 * Cfg::SUPER : (ub + 7) / 8 * 8;
-  grouped_gemm_kernel<T, Cfg, MODE><<<dim3((unsigned)grid), Cfg::THREADS, Cfg::LDS_BYTES, st>>>(
-      x, w, y, H, I, topk, R, E, ntn, sorted, offsets, t_exp, t_ms, meta);
+  grouped_gemm_kernel<T, Cfg, MODE, EPI><<<dim3((unsigned)grid), Cfg::THREADS, Cfg::LDS_BYTES, st>>>(
+      x, w, w2, y, H, I, topk, R, E, ntn, sorted, offsets, t_exp, t_ms, meta);
   return MOE_OK;
 }
 
@@ -446,27 +474,32 @@ extern "C" size_t moe_grouped_gemm_workspace_size(int64_t T, int64_t topk, int64
   return kWsCtlBytes + gemm_layout(T * topk, E).total;
 }
 
-extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert_ids, int dtype,
-                                int idx_dtype, int64_t T, int64_t topk, int64_t H, int64_t I,
-                                int64_t E, void* Y, void* workspace, size_t ws_bytes, void* stream) {
-  if (T < 0 || topk < 1 || H < 1 || I < 1)
-    return fail(MOE_EINVAL, "grouped_gemm: need T >= 0, topk >= 1, H >= 1, I >= 1");
-  if (E < 1 || E > kMaxExperts) return fail(MOE_EUNSUP, "grouped_gemm: need 1 <= E <= 4096");
-  if (H % 8 != 0) return fail(MOE_EUNSUP, "grouped_gemm: H must be a multiple of 8");
+namespace moe {
+
+// Shared by moe_grouped_gemm (EPI 0) and moe_grouped_gemm_swiglu (EPI 1,
+// W2 = the up weights; I is the output width, the tile rows cover 2 I).
+template <int EPI>
+static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const void* W2, const void* expert_ids,
+                             int dtype, int idx_dtype, int64_t T, int64_t topk, int64_t H, int64_t I, int64_t E,
+                             void* Y, void* workspace, size_t ws_bytes, void* stream) {
+  const std::string f(fn);
+  if (T < 0 || topk < 1 || H < 1 || I < 1) return fail(MOE_EINVAL, f + ": need T >= 0, topk >= 1, H >= 1, I >= 1");
+  if (E < 1 || E > kMaxExperts) return fail(MOE_EUNSUP, f + ": need 1 <= E <= 4096");
+  if (H % 8 != 0) return fail(MOE_EUNSUP, f + ": H must be a multiple of 8");
   const int64_t R = T * topk;
-  if (R >= INT32_MAX || (R + kMinBM - 1) / kMinBM + E + 1 > (int64_t)INT32_MAX / ((I + 63) / 64))
-    return fail(MOE_EUNSUP, "grouped_gemm: problem too large");
+  const int64_t Iv = EPI == 1 ? 2 * I : I;  // weight rows per expert the tiles walk
+  if (R >= INT32_MAX || (R + kMinBM - 1) / kMinBM + E + 1 > (int64_t)INT32_MAX / ((Iv + 63) / 64))
+    return fail(MOE_EUNSUP, f + ": problem too large");
   if (dtype != MOE_BF16 && dtype != MOE_F16)
-    return fail(MOE_EINVAL, "grouped_gemm: X, W and Y must be bfloat16 or float16");
-  if (idx_dtype != MOE_I32 && idx_dtype != MOE_I64)
-    return fail(MOE_EINVAL, "grouped_gemm: expert ids must be int32 or int64");
+    return fail(MOE_EINVAL, f + ": X, W and Y must be bfloat16 or float16");
+  if (idx_dtype != MOE_I32 && idx_dtype != MOE_I64) return fail(MOE_EINVAL, f + ": expert ids must be int32 or int64");
   if (R == 0) return MOE_OK;
-  if (!X || !W || !expert_ids || !Y) return fail(MOE_EINVAL, "grouped_gemm: null pointer");
-  if (((uintptr_t)X | (uintptr_t)W) & 15)
-    return fail(MOE_EINVAL, "grouped_gemm: X and W must be 16-byte aligned");
+  if (!X || !W || !expert_ids || !Y || (EPI == 1 && !W2)) return fail(MOE_EINVAL, f + ": null pointer");
+  if (((uintptr_t)X | (uintptr_t)W | (uintptr_t)W2) & 15)
+    return fail(MOE_EINVAL, f + ": X and the weights must be 16-byte aligned");
   const GemmLayout g = gemm_layout(R, E);
   if (!workspace || ws_bytes < kWsCtlBytes + g.total)
-    return fail(MOE_EINVAL, "grouped_gemm: workspace too small (" + std::to_string(ws_bytes) + " < " +
+    return fail(MOE_EINVAL, f + ": workspace too small (" + std::to_string(ws_bytes) + " < " +
                                 std::to_string(kWsCtlBytes + g.total) + ")");
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace) + kWsCtlBytes;
@@ -480,7 +513,7 @@ extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert
   // The largest tiles that still give every CU about two of them: 256x256
   // (BK 64, full 128-byte lines per row copy) moves the least data per
   // MFMA; smaller problems take smaller tiles to fill the chip.
-  auto tiles_of = [&](int64_t bm, int64_t bn) { return ((R + bm - 1) / bm) * ((I + bn - 1) / bn); };
+  auto tiles_of = [&](int64_t bm, int64_t bn) { return ((R + bm - 1) / bm) * ((Iv + bn - 1) / bn); };
   const int cfg = tiles_of(CfgHuge::BM, CfgHuge::BN) >= 512 ? 2 : tiles_of(CfgLarge::BM, CfgLarge::BN) >= 512 ? 1 : 0;
   const int bm = cfg == 2 ? CfgHuge::BM : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
   const int bn = cfg == 2 ? CfgHuge::BN : cfg == 1 ? CfgLarge::BN : CfgSmall::BN;
@@ -492,17 +525,38 @@ extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert
     rc = launch_route(static_cast<const int32_t*>(expert_ids), R, (int)E, blockcnt, counts, offsets, sorted,
                       bm, t_exp, t_ms, meta, st);
   if (rc) return rc;
-  const int ntn = (int)((I + bn - 1) / bn);
+  const int obn = EPI == 1 ? bn / 2 : bn;
+  const int ntn = (int)((I + obn - 1) / obn);
   const uint16_t* x = static_cast<const uint16_t*>(X);
   const uint16_t* w = static_cast<const uint16_t*>(W);
+  const uint16_t* w2 = static_cast<const uint16_t*>(W2);
   uint16_t* y = static_cast<uint16_t*>(Y);
   auto run = [&](auto cfg_tag) {
     using C = decltype(cfg_tag);
     return dtype == MOE_BF16
-               ? launch_gemm<uint16_t, C>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta)
-               : launch_gemm<Half16, C>(st, x, w, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets, t_exp, t_ms, meta);
+               ? launch_gemm<uint16_t, C, 0, EPI>(st, x, w, w2, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets,
+                                                 t_exp, t_ms, meta)
+               : launch_gemm<Half16, C, 0, EPI>(st, x, w, w2, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets,
+                                               t_exp, t_ms, meta);
   };
   rc = cfg == 2 ? run(CfgHuge{}) : cfg == 1 ? run(CfgLarge{}) : run(CfgSmall{});
   if (rc) return rc;
   return check_launch("grouped_gemm_kernel");
+}
+
+}  // namespace moe
+
+extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert_ids, int dtype,
+                                int idx_dtype, int64_t T, int64_t topk, int64_t H, int64_t I,
+                                int64_t E, void* Y, void* workspace, size_t ws_bytes, void* stream) {
+  return grouped_gemm_impl<0>("grouped_gemm", X, W, nullptr, expert_ids, dtype, idx_dtype, T, topk, H, I, E, Y,
+                              workspace, ws_bytes, stream);
+}
+
+extern "C" int moe_grouped_gemm_swiglu(const void* X, const void* Wg, const void* Wu, const void* expert_ids,
+                                       int dtype, int idx_dtype, int64_t T, int64_t topk, int64_t H,
+                                       int64_t I, int64_t E, void* Y, void* workspace, size_t ws_bytes,
+                                       void* stream) {
+  return grouped_gemm_impl<1>("grouped_gemm_swiglu", X, Wg, Wu, expert_ids, dtype, idx_dtype, T, topk, H, I, E, Y,
+                              workspace, ws_bytes, stream);
 }

@@ -26,6 +26,17 @@ from .topk_softmax import (
     topk_softmax_sonic,
 )
 from .grouped_gemm import grouped_gemm, grouped_gemm_best, route_sort
+from .fusedmoe import (
+    FusedMoETileLang,
+    FusedMoETileLangStreams,
+    fused_moe_routed,
+    fusedmoe,
+    fusedmoe_best,
+    fusedmoe_tilelang,
+    fusedmoe_tilelang_streams,
+    grouped_gemm_swiglu,
+    moe_combine,
+)
 from .router_gemm_topk_softmax import (
     get_fused_router_kernel,
     get_router_gemm_kernel,
@@ -56,4 +67,13 @@ __all__ = [
     "router_topk_softmax",
     "get_router_gemm_kernel",
     "get_fused_router_kernel",
+    "fusedmoe",
+    "fusedmoe_best",
+    "fusedmoe_tilelang",
+    "fusedmoe_tilelang_streams",
+    "FusedMoETileLang",
+    "FusedMoETileLangStreams",
+    "fused_moe_routed",
+    "grouped_gemm_swiglu",
+    "moe_combine",
 ]
