@@ -37,13 +37,30 @@ constexpr size_t kWsCtlBytes = 4096;
 #ifdef MOE_PHASE_TIMING
 #define MOE_PHASE(slot)                                                        \
   do {                                                                         \
-    if (threadIdx.x == 0) moe_phase[blockIdx.x * 16 + (slot)] = wall_clock64(); \
+    if (threadIdx.x == 0) moe_phase[blockIdx.x * 32 + (slot)] = wall_clock64(); \
+  } while (0)
+#define MOE_PHASE_T(slot, t)                                                   \
+  do {                                                                         \
+    if (threadIdx.x == (t)) moe_phase[blockIdx.x * 32 + (slot)] = wall_clock64(); \
   } while (0)
 #else
 #define MOE_PHASE(slot) \
   do {                  \
   } while (0)
+#define MOE_PHASE_T(slot, t) \
+  do {                       \
+  } while (0)
 #endif
+
+// Workgroup barrier that orders LDS only.  __syncthreads() carries a
+// workgroup fence over every address space, which waits for all of the
+// wave's outstanding global loads (vmcnt(0)); this one waits for LDS
+// traffic alone (lgkmcnt(0)), so row loads issued earlier stay in flight.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // ---------------------------------------------------------------------------
 // Order-preserving 32-bit keys.  key(a) > key(b)  <=>  a > b, with -0.0 and

@@ -234,7 +234,7 @@ __device__ inline void radix_pick_bin_w0(RadixState& st, const uint32_t* hist, i
       s_pick[2] = v;
     }
   }
-  __syncthreads();
+  lds_barrier();
   const uint32_t bin = s_pick[0];
   st.need -= s_pick[1];
   st.prefix |= bin << sh;
@@ -369,19 +369,22 @@ __device__ inline uint32_t sample_bound(uint32_t samp, int K, int N, uint32_t* h
   if (m_rank >= kSample) return 1u;  // no useful bound: every real key
   const int tid = threadIdx.x;
   for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
-  __syncthreads();
+  lds_barrier();
+  MOE_PHASE(6);
   wave_aggregated_add(hist, samp >> 21, true, 11);
-  __syncthreads();
+  lds_barrier();
+  MOE_PHASE(7);
   RadixState ss{0u, 0u, (uint32_t)m_rank, 0u, false};
   radix_pick_bin_w0(ss, hist, 21, 0x7FFu, s_pick);
+  MOE_PHASE(15);
   // Samples at or above the bin's lower edge estimate the candidate count.
   const uint32_t at_or_above = (uint32_t)m_rank - ss.need + ss.eq_count;
   if (!ss.all_taken && (float)at_or_above * ((float)N / kSample) > 0.5f * kCandCap) {
     for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
-    __syncthreads();
+    lds_barrier();
     const bool in = (samp & ss.fixed) == ss.prefix;
     if (__ballot(in)) wave_aggregated_add(hist, (samp >> 10) & 0x7FFu, in, 11);
-    __syncthreads();
+    lds_barrier();
     radix_pick_bin_w0(ss, hist, 10, 0x7FFu, s_pick);
   }
   return max(ss.prefix, 1u);
@@ -407,25 +410,46 @@ __device__ inline uint64_t wave_sum_u64(uint64_t v) {
   return v;
 }
 
+// Clears what order_and_store expects zeroed (the bucket counts and the
+// crowding flag).  Callers run it before the barrier that publishes cand[].
+__device__ inline void order_prepare(uint32_t* hist, uint32_t* s_flag) {
+  for (int b = threadIdx.x; b < kOrdBuckets; b += kRadixThreads) hist[b] = 0;
+  if (threadIdx.x == 0) *s_flag = 0;
+}
+
 // Orders the C candidates in cand[] (LDS, distinct composites, the K largest
 // among them are the row's winners), applies the softmax and stores row
-// `row`.  tmp needs kCandCap entries, hist and bstart kOrdBuckets + 1.
-template <typename IdxT>
-__device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uint32_t rmax, int K,
-                                       int64_t row, uint64_t* tmp, uint32_t* hist, uint32_t* bstart,
-                                       uint32_t* wsum, uint32_t* s_flag, float* s_red,
-                                       float* scores, IdxT* indices, uint64_t* s_sum64) {
-  constexpr int CPT = kCandCap / kRadixThreads;  // candidates per thread, max
+// `row`.  Thread t owns candidates t + 1024 u, u < U (U * 1024 >= C), and
+// keeps them, their buckets and their ranks in registers from the first
+// step to the last, so every step issues its U LDS accesses together.
+// hist[] and *s_flag must be zero (order_prepare) and published by a
+// barrier; tmp needs kCandCap entries, hist and bstart kOrdBuckets + 1.
+template <int U, typename IdxT>
+__device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t* cand, int C, uint32_t base, uint32_t rmax, int K,
+                                         int64_t row, uint64_t* tmp, uint32_t* hist, uint32_t* bstart,
+                                         uint32_t* wsum, uint32_t* s_flag, float* s_red,
+                                         float* scores, IdxT* indices, uint64_t* s_sum64) {
+  uint32_t* s_cw = s_flag + 1;  // candidates in the buckets that can win (s_flag[2])
   constexpr int BPT = kOrdBuckets / kRadixThreads;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   int sh = 0;
   while (((rmax - base) >> sh) >= (uint32_t)kOrdBuckets) ++sh;
   auto bucket = [&](uint64_t v) { return kOrdBuckets - 1 - (int)((comp_key(v) - base) >> sh); };
+  uint64_t v[U];
+  int bk[U];
+  bool in[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int p = tid + kRadixThreads * u;
+    in[u] = p < C;
+    v[u] = in[u] ? cand[p] : 0ull;
+  }
   MOE_PHASE(8);
-  for (int b = tid; b < kOrdBuckets; b += kRadixThreads) hist[b] = 0;
-  if (tid == 0) *s_flag = 0;
-  __syncthreads();
-  for (int p = tid; p < C; p += kRadixThreads) atomicAdd(&hist[bucket(cand[p])], 1u);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    bk[u] = bucket(v[u]);
+    if (in[u]) atomicAdd(&hist[bk[u]], 1u);
+  }
   __syncthreads();
   MOE_PHASE(9);
   {
@@ -441,6 +465,8 @@ __device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uin
     for (int q = 0; q < BPT; ++q) {
       bstart[tid * BPT + q] = run;
       hist[tid * BPT + q] = run;  // cursor
+      // The bucket holding rank K - 1 ends the candidates that can win.
+      if (run < (uint32_t)K && (uint32_t)K <= run + h[q]) *s_cw = run + h[q];
       run += h[q];
     }
     if (tid == 0) bstart[kOrdBuckets] = (uint32_t)C;
@@ -450,7 +476,7 @@ __device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uin
   __syncthreads();
   MOE_PHASE(10);
   if (*s_flag) {
-    // Crowded bucket: sort all candidates instead.
+    // Crowded bucket: sort all candidates instead (cand[] is intact).
     const int Cpad = next_pow2_dev(C);
     for (int p = C + tid; p < Cpad; p += kRadixThreads) cand[p] = 0;
     __syncthreads();
@@ -458,30 +484,42 @@ __device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uin
     radix_epilogue(cand, K, row, s_red, scores, indices);
     return;
   }
-  for (int p = tid; p < C; p += kRadixThreads) {
-    const uint64_t v = cand[p];
-    tmp[atomicAdd(&hist[bucket(v)], 1u)] = v;
-  }
+  // Only buckets that start below rank K can hold winners: the others are
+  // neither placed nor ranked.
+  const int Cw = (int)*s_cw;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (in[u] && (int)bstart[bk[u]] < K) tmp[atomicAdd(&hist[bk[u]], 1u)] = v[u];
   __syncthreads();
   MOE_PHASE(11);
-  const float vmax = value_of_key(rmax);
-  int rk[CPT];
-  float ex[CPT];
-  uint32_t ix[CPT];
+  // Rank = bucket start + larger composites in the bucket (buckets hold at
+  // most kBucketFixMax candidates).  Thread t now ranks the candidates at
+  // sorted positions t + 1024 u < Cw, so the lanes of a wave share buckets.
+  int beg[U], len[U], rk[U], lmax = 0;
 #pragma unroll
-  for (int u = 0; u < CPT; ++u) {
-    const int p = tid + kRadixThreads * u;
-    rk[u] = K;
-    if (p < C) {
-      const uint64_t v = tmp[p];
-      const int rb = bucket(v);
-      const int beg = (int)bstart[rb], end = (int)bstart[rb + 1];
-      int r = beg;
-      for (int q = beg; q < end; ++q) r += tmp[q] > v;
-      rk[u] = r;
-      ix[u] = comp_idx(v);
-      ex[u] = expf(value_of_key(comp_key(v)) - vmax);
-    }
+  for (int u = 0; u < U; ++u) {
+    in[u] = tid + kRadixThreads * u < Cw;
+    v[u] = in[u] ? tmp[tid + kRadixThreads * u] : 0ull;
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int b = bucket(v[u]);
+    beg[u] = in[u] ? (int)bstart[b] : 0;
+    len[u] = in[u] ? (int)bstart[b + 1] - beg[u] : 0;
+    rk[u] = beg[u];
+    lmax = max(lmax, len[u]);
+  }
+  // Four in-bucket loads per candidate are in flight before any compare.
+  for (int j = 0; j < lmax; j += 4) {
+    uint64_t t[U][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) t[u][q] = j + q < len[u] ? tmp[beg[u] + j + q] : 0ull;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) rk[u] += t[u][q] > v[u];
   }
   MOE_PHASE(12);
   // The normaliser is summed exactly, in fixed point, so the scores are
@@ -490,14 +528,20 @@ __device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uin
   // round-down multiples of 2^-48 (error <= K 2^-48 relative to a sum >= 1)
   // and added as uint64, which is associative.  A NaN exp (a NaN or +inf
   // in the row) makes every score NaN, as in torch.softmax.
+  // Each winner's exp and column are staged in cand[] at its rank (cand[] is
+  // no longer read), so the row is stored with coalesced writes.
+  const float vmax = value_of_key(rmax);
   uint64_t qsum = 0;
   bool nan = false;
 #pragma unroll
-  for (int u = 0; u < CPT; ++u)
-    if (rk[u] < K) {
-      qsum += fixed48(ex[u]);
-      nan |= ex[u] != ex[u];
+  for (int u = 0; u < U; ++u) {
+    if (in[u] && rk[u] < K) {
+      const float ex = expf(value_of_key(comp_key(v[u])) - vmax);
+      qsum += fixed48(ex);
+      nan |= ex != ex;
+      cand[rk[u]] = ((uint64_t)__float_as_uint(ex) << 32) | comp_idx(v[u]);
     }
+  }
   qsum = wave_sum_u64(qsum);
   if (lane == 0) s_sum64[tid / kWave] = __ballot(nan) ? ~0ull : qsum;
   __syncthreads();
@@ -511,11 +555,29 @@ __device__ inline void order_and_store(uint64_t* cand, int C, uint32_t base, uin
     total += q;
   }
   const float sum = any_nan ? __builtin_nanf("") : (float)((double)total * 0x1p-48);
-  (void)s_red;
-#pragma unroll
-  for (int u = 0; u < CPT; ++u)
-    if (rk[u] < K) store_out(scores, indices, row * K + rk[u], ex[u] / sum, ix[u]);
+  for (int r = tid; r < K; r += kRadixThreads) {
+    const uint64_t e = cand[r];
+    store_out(scores, indices, row * K + r, __uint_as_float((uint32_t)(e >> 32)) / sum, (uint32_t)e);
+  }
   MOE_PHASE(14);
+}
+
+template <typename IdxT>
+__device__ __attribute__((always_inline)) inline void order_and_store(uint64_t* cand, int C, uint32_t base, uint32_t rmax, int K,
+                                       int64_t row, uint64_t* tmp, uint32_t* hist, uint32_t* bstart,
+                                       uint32_t* wsum, uint32_t* s_flag, float* s_red,
+                                       float* scores, IdxT* indices, uint64_t* s_sum64) {
+  static_assert(kCandCap == 8 * kRadixThreads, "order_and_store covers 8 candidates per thread");
+  const int units = (C + kRadixThreads - 1) / kRadixThreads;
+#define MOE_ORDER_U(n) \
+  order_and_store_u<n, IdxT>(cand, C, base, rmax, K, row, tmp, hist, bstart, wsum, s_flag, s_red, scores, indices, s_sum64)
+  if (units <= 1) MOE_ORDER_U(1);
+  else if (units == 2) MOE_ORDER_U(2);
+  else if (units == 3) MOE_ORDER_U(3);
+  else if (units == 4) MOE_ORDER_U(4);
+  else if (units <= 6) MOE_ORDER_U(6);
+  else MOE_ORDER_U(8);
+#undef MOE_ORDER_U
 }
 
 // Row slice [c0, end) of thread tid: columns c0 + VEC*(tid + 1024*j) + c,
@@ -678,7 +740,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   __shared__ uint32_t bstart[kOrdBuckets + 1];
   __shared__ uint32_t wsum[kRadixThreads / kWave];
   __shared__ uint32_t s_pick[3];
-  __shared__ uint32_t s_max, s_flag;
+  __shared__ uint32_t s_max, s_flag[2];  // crowding flag, winner-bucket count
   __shared__ uint64_t s_sum64[kRadixThreads / kWave];
   __shared__ float s_red[kRadixThreads / kWave];
 
@@ -688,6 +750,8 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   const T* x = logits + row * ld;
 
   MOE_PHASE(0);
+  MOE_PHASE_T(16, 1023);
+  MOE_PHASE_T(17, 512);
   // The sample load goes first so that the bound waits for it alone while
   // the row loads are still in flight.
   const uint32_t samp = sample_key(x, N);
@@ -782,9 +846,10 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
 #pragma unroll
   for (int i = 0; i < KPT; ++i)
     if ((mask >> i) & 1u) cand[cpos++] = make_comp(key[i], slot_col<VEC>(0, i));
+  order_prepare(hist, s_flag);
   __syncthreads();
   MOE_PHASE(4);
-  order_and_store(cand, (int)C, base, rmax, K, row, tmp, hist, bstart, wsum, &s_flag, s_red, scores, indices,
+  order_and_store(cand, (int)C, base, rmax, K, row, tmp, hist, bstart, wsum, s_flag, s_red, scores, indices,
                   s_sum64);
   MOE_PHASE(5);
 }
@@ -826,7 +891,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   __shared__ uint32_t bstart[kOrdBuckets + 1];
   __shared__ uint32_t wsum[kRadixThreads / kWave];
   __shared__ uint32_t s_pick[3];
-  __shared__ uint32_t s_max, s_flag, s_base, s_last;
+  __shared__ uint32_t s_max, s_base, s_last, s_flag[2];  // s_flag: crowding flag, winner-bucket count
   __shared__ uint64_t s_sum64[kRadixThreads / kWave];
   __shared__ float s_red[kRadixThreads / kWave];
 
@@ -903,16 +968,17 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
     __hip_atomic_store(&rc->rmax, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (C < (uint32_t)K || C > (uint32_t)kCandCap) {
-    radix_row_global<T, IdxT>(x, N, K, Kpad, row, cand, hist, wsum, s_pick, &s_flag, s_red, scores, indices);
+    radix_row_global<T, IdxT>(x, N, K, Kpad, row, cand, hist, wsum, s_pick, s_flag, s_red, scores, indices);
     return;
   }
   // Agent-scope atomic loads read past this XCD's L2 copy, so they see every
   // workgroup's candidates.
   for (uint32_t p = tid; p < C; p += kRadixThreads)
     cand[p] = __hip_atomic_load(rcand + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  order_prepare(hist, s_flag);
   __syncthreads();
   MOE_PHASE(6);
-  order_and_store(cand, (int)C, L, rmax, K, row, tmp, hist, bstart, wsum, &s_flag, s_red, scores, indices,
+  order_and_store(cand, (int)C, L, rmax, K, row, tmp, hist, bstart, wsum, s_flag, s_red, scores, indices,
                   s_sum64);
   MOE_PHASE(7);
 }
