@@ -32,23 +32,27 @@ constexpr int kWave = 64;
 // entry point in turn on one stream.
 constexpr size_t kWsCtlBytes = 4096;
 
-// Phase timestamps for kernel tuning builds (-DMOE_PHASE_TIMING): thread 0
-// of each workgroup records the wall clock into moe_phase[block][slot].
+// Phase timestamps for kernel tuning builds (-DMOE_PHASE_TIMING, which
+// also provides moe_phase[] and moe_phase_lds[]): thread 0 of each
+// workgroup records the wall clock of phase `slot` in LDS, and
+// MOE_PHASE_FLUSH() copies the record to moe_phase[block][slot] once, so
+// the timestamps add no global stores (which barriers would wait for)
+// inside the timed phases.
 #ifdef MOE_PHASE_TIMING
-#define MOE_PHASE(slot)                                                        \
-  do {                                                                         \
-    if (threadIdx.x == 0) moe_phase[blockIdx.x * 32 + (slot)] = wall_clock64(); \
+#define MOE_PHASE(slot)                                              \
+  do {                                                               \
+    if (threadIdx.x == 0) moe_phase_lds[(slot)] = wall_clock64();    \
   } while (0)
-#define MOE_PHASE_T(slot, t)                                                   \
-  do {                                                                         \
-    if (threadIdx.x == (t)) moe_phase[blockIdx.x * 32 + (slot)] = wall_clock64(); \
+#define MOE_PHASE_FLUSH()                                            \
+  do {                                                               \
+    if (threadIdx.x < 32) moe_phase[blockIdx.x * 32 + threadIdx.x] = moe_phase_lds[threadIdx.x]; \
   } while (0)
 #else
 #define MOE_PHASE(slot) \
   do {                  \
   } while (0)
-#define MOE_PHASE_T(slot, t) \
-  do {                       \
+#define MOE_PHASE_FLUSH() \
+  do {                    \
   } while (0)
 #endif
 

@@ -370,13 +370,13 @@ __device__ inline uint32_t sample_bound(uint32_t samp, int K, int N, uint32_t* h
   const int tid = threadIdx.x;
   for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
   lds_barrier();
-  MOE_PHASE(6);
+  MOE_PHASE(16);
   wave_aggregated_add(hist, samp >> 21, true, 11);
   lds_barrier();
-  MOE_PHASE(7);
+  MOE_PHASE(17);
   RadixState ss{0u, 0u, (uint32_t)m_rank, 0u, false};
   radix_pick_bin_w0(ss, hist, 21, 0x7FFu, s_pick);
-  MOE_PHASE(15);
+  MOE_PHASE(18);
   // Samples at or above the bin's lower edge estimate the candidate count.
   const uint32_t at_or_above = (uint32_t)m_rank - ss.need + ss.eq_count;
   if (!ss.all_taken && (float)at_or_above * ((float)N / kSample) > 0.5f * kCandCap) {
@@ -750,8 +750,6 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   const T* x = logits + row * ld;
 
   MOE_PHASE(0);
-  MOE_PHASE_T(16, 1023);
-  MOE_PHASE_T(17, 512);
   // The sample load goes first so that the bound waits for it alone while
   // the row loads are still in flight.
   const uint32_t samp = sample_key(x, N);
@@ -852,6 +850,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   order_and_store(cand, (int)C, base, rmax, K, row, tmp, hist, bstart, wsum, s_flag, s_red, scores, indices,
                   s_sum64);
   MOE_PHASE(5);
+  MOE_PHASE_FLUSH();
 }
 
 // ===========================================================================
@@ -981,6 +980,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   order_and_store(cand, (int)C, L, rmax, K, row, tmp, hist, bstart, wsum, s_flag, s_red, scores, indices,
                   s_sum64);
   MOE_PHASE(7);
+  MOE_PHASE_FLUSH();
 }
 
 // ===========================================================================
