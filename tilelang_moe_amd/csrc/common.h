@@ -25,6 +25,12 @@ int check_launch(const char* what);
                                        hipGetErrorString(_e));                 \
   } while (0)
 
+// Top-K + softmax (Convention B) of the rows sum_g part[g][M][N], g in
+// order 0..G-1 (fp32 partials of a split-H router GEMM), N <= 256; one wave
+// per row.  Defined with the selection kernel (router.hip).
+int topk_select_partials(const float* part, int G, int64_t M, int N, int K, float* scores, void* indices,
+                         int idx_dtype, hipStream_t st);
+
 constexpr int kWave = 64;
 // Every workspace starts with a control block of this size: the only bytes
 // that must be zero before a call, and every call leaves them zero.  Scratch

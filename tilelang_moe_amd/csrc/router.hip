@@ -85,11 +85,14 @@ __global__ __launch_bounds__(256) void topk_bitonic_kernel(const T* __restrict__
 //    unique 64-bit composites and the winner is cleared in place.
 //    The K winners are staged in LDS for the softmax epilogue.
 // ===========================================================================
-template <typename T, int EPL, typename IdxT>
+// With PSUM (fp32 rows only) the row is the sum, in order g = 0..G-1, of the
+// G partial rows logits + g * gstride (split-H router GEMM partials).
+template <typename T, int EPL, typename IdxT, bool PSUM = false>
 __global__ __launch_bounds__(256) void topk_select_kernel(const T* __restrict__ logits,
                                                           int64_t M, int N, int64_t ld,
                                                           int K, float* __restrict__ scores,
-                                                          IdxT* __restrict__ indices) {
+                                                          IdxT* __restrict__ indices, int G = 1,
+                                                          int64_t gstride = 0) {
   extern __shared__ uint64_t win_all[];  // [waves][K]
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -99,10 +102,41 @@ __global__ __launch_bounds__(256) void topk_select_kernel(const T* __restrict__ 
   const T* x = logits + (live ? row : 0) * ld;
 
   uint64_t c[EPL];
+  if constexpr (PSUM) {
+    static_assert(sizeof(T) == 4, "partial sums are fp32");
+    float v[EPL];
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const int idx = lane + kWave * i;
-    c[i] = (live && idx < N) ? make_comp(key_of_bits(Elem<T>::bits(x + idx)), idx) : 0;
+    for (int i = 0; i < EPL; ++i) {
+      const int idx = lane + kWave * i;
+      v[i] = (live && idx < N) ? x[idx] : 0.0f;
+    }
+    // Eight partial rows in flight at a time, added in split order.
+    for (int g0 = 1; g0 < G; g0 += 8) {
+      float p[8][EPL];
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+          const int idx = lane + kWave * i;
+          p[q][i] = (live && idx < N && g0 + q < G) ? x[(size_t)(g0 + q) * gstride + idx] : 0.0f;
+        }
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+          if (g0 + q < G) v[i] += p[q][i];
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int idx = lane + kWave * i;
+      c[i] = (live && idx < N) ? make_comp(key_of_bits(__float_as_uint(v[i])), idx) : 0;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int idx = lane + kWave * i;
+      c[i] = (live && idx < N) ? make_comp(key_of_bits(Elem<T>::bits(x + idx)), idx) : 0;
+    }
   }
 
   for (int r = 0; r < K; ++r) {
@@ -1045,6 +1079,35 @@ static void launch_select_e(const T* x, int64_t M, int N, int64_t ld, int K, flo
   const size_t lds = (size_t)waves * K * sizeof(uint64_t);
   topk_select_kernel<T, EPL, IdxT><<<dim3((unsigned)grid), dim3(waves * kWave), lds, st>>>(
       x, M, N, ld, K, s, id);
+}
+
+template <typename IdxT, int EPL>
+static void launch_select_psum_e(const float* part, int G, int64_t M, int N, int K, float* s, IdxT* id,
+                                 hipStream_t st) {
+  const int waves = 4;
+  const int64_t grid = (M + waves - 1) / waves;
+  const size_t lds = (size_t)waves * K * sizeof(uint64_t);
+  topk_select_kernel<float, EPL, IdxT, true><<<dim3((unsigned)grid), dim3(waves * kWave), lds, st>>>(
+      part, M, N, N, K, s, id, G, M * N);
+}
+
+template <typename IdxT>
+static int launch_select_psum(const float* part, int G, int64_t M, int N, int K, float* s, IdxT* id,
+                              hipStream_t st) {
+  const int epl = (N + kWave - 1) / kWave;
+  if (epl <= 1) launch_select_psum_e<IdxT, 1>(part, G, M, N, K, s, id, st);
+  else if (epl <= 2) launch_select_psum_e<IdxT, 2>(part, G, M, N, K, s, id, st);
+  else if (epl <= 4) launch_select_psum_e<IdxT, 4>(part, G, M, N, K, s, id, st);
+  else return fail(MOE_EUNSUP, "partial-sum selection supports N <= 256");
+  return check_launch("topk_select_kernel");
+}
+
+int topk_select_partials(const float* part, int G, int64_t M, int N, int K, float* scores, void* indices,
+                         int idx_dtype, hipStream_t st) {
+  if (M == 0) return MOE_OK;
+  if (K > N || G < 1) return fail(MOE_EINVAL, "topk_select_partials: need K <= N and G >= 1");
+  if (idx_dtype == MOE_I64) return launch_select_psum(part, G, M, N, K, scores, static_cast<int64_t*>(indices), st);
+  return launch_select_psum(part, G, M, N, K, scores, static_cast<int32_t*>(indices), st);
 }
 
 template <typename T, typename IdxT>

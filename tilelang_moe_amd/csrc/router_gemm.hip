@@ -10,11 +10,13 @@
 // then both MFMA operands are K-contiguous rows and the tile k loop is the
 // grouped GEMM's LDS-DMA pipeline (mfma_tile.h) unchanged.  A block owns
 // BM = 64 tokens x BN (128 or 256) experts.  When the token count gives
-// fewer tiles than CUs, H is split over G blocks per tile: each stores its
-// partial tile with agent-scope atomic stores, and the last block to count
-// in sums the G partials in split order (deterministic) and writes the
-// logits; the fused entry point then runs the selection kernel on them
-// (split plans have too few tiles for a per-tile selection epilogue).
+// fewer tiles than CUs, H is split over G blocks per tile: block g stores its
+// partial logits row-major in part[g][T][E] and is done.  The sum of the G
+// partials, in split order (deterministic), is taken by whoever reads the
+// logits next, spread over many workgroups: router_reduce_kernel for the
+// logits entry point, the selection kernel itself (topk_select_partials)
+// for the fused one.  (Split plans have too few tiles for a per-tile
+// selection epilogue.)
 //
 // Fused epilogue (unsplit plans): the tile's logits go to LDS; a 16-lane
 // segment selects one row (lane pos holds the keys of columns pos + 16 i):
@@ -130,25 +132,17 @@ using CfgRouter128 = GemmCfg<64, 128, 2, 2, 64, 3>;     // 4 waves of 32x64, 72 
 using CfgRouter256 = GemmCfg<64, 256, 1, 4, 64, 2>;     // 4 waves of 64x64, 80 KB LDS
 constexpr int kRouterSeg = 16;                         // lanes per row in the fused epilogue
 constexpr int kRouterMaxK = 2 * kRouterSeg;            // winners held two per lane
-constexpr int64_t kRouterMinSplitK = 512;              // fewest k per split
+constexpr int64_t kRouterMinSplitK = 256;              // fewest k per split
 
-template <typename Cfg>
-struct RouterLayout {
-  static constexpr int PART = Cfg::FM * Cfg::FN * 16;  // accumulators per thread
-  static constexpr size_t TILE_FLOATS = (size_t)Cfg::THREADS * PART;
-  static_assert((size_t)Cfg::BM * Cfg::BN * 4 <= Cfg::LDS_BYTES, "logits tile must fit the stage ring");
-};
 
 // EPI 0: logits[T,E] fp32.  EPI 1: scores/indices [T,K] (requires one N tile).
 template <typename T, typename Cfg, int EPI, typename IdxT>
 __global__ __launch_bounds__(Cfg::THREADS) void router_gemm_kernel(
     const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, int64_t Tn, int64_t H, int E, int K,
     int NT, int G, int64_t kchunk, float* __restrict__ logits, float* __restrict__ scores,
-    IdxT* __restrict__ indices, float* __restrict__ part, uint32_t* __restrict__ counters) {
+    IdxT* __restrict__ indices, float* __restrict__ part) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, CPR = Cfg::CPR;
-  using L = RouterLayout<Cfg>;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  __shared__ uint32_t s_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -190,45 +184,13 @@ __global__ __launch_bounds__(Cfg::THREADS) void router_gemm_kernel(
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
   tile_mainloop<T, Cfg, 0>(smem, a_src, b_src, cchunk, kb, ke, fm_act, acc);
 
-  if (G > 1) {
-    // Publish this split's partial tile (thread-major: coalesced), count
-    // in; the last split sums all G in split order.
-    float* mine = part + ((size_t)t * G + g) * L::TILE_FLOATS;
-#pragma unroll
-    for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-      for (int j = 0; j < Cfg::FN; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          __hip_atomic_store(mine + (size_t)((i * Cfg::FN + j) * 16 + v) * Cfg::THREADS + tid, acc[i][j][v],
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // these agent-scope stores write through L2
-    __syncthreads();
-    if (tid == 0)
-      s_last = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(G - 1);
-    __syncthreads();
-    if (!s_last) return;
-    if (tid == 0) __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int q = 0; q < G; ++q) {
-      const float* src = part + ((size_t)t * G + q) * L::TILE_FLOATS;
-#pragma unroll
-      for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < Cfg::FN; ++j)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const float p = __hip_atomic_load(src + (size_t)((i * Cfg::FN + j) * 16 + v) * Cfg::THREADS + tid,
-                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            acc[i][j][v] = q == 0 ? p : acc[i][j][v] + p;
-          }
-    }
-  }
-
   // Accumulator v of lane l: row 8*(v/4) + 4*(l/32) + v%4, column l%32 of
   // its 32x32 block.
   auto row_of = [&](int i, int v) { return (wm * Cfg::FM + i) * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); };
   auto col_of = [&](int j) { return (wn * Cfg::FN + j) * 32 + (lane & 31); };
   if constexpr (EPI == 0) {
+    // Unsplit: the logits.  Split: this block's partial, part[g][T][E].
+    float* dst = G > 1 ? part + (size_t)g * Tn * E : logits;
 #pragma unroll
     for (int i = 0; i < Cfg::FM; ++i)
 #pragma unroll
@@ -237,7 +199,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void router_gemm_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int64_t r = m0 + row_of(i, v);
-          if (r < Tn && c < E) logits[r * E + c] = acc[i][j][v];
+          if (r < Tn && c < E) dst[r * E + c] = acc[i][j][v];
         }
       }
     return;
@@ -320,6 +282,28 @@ __global__ __launch_bounds__(Cfg::THREADS) void router_gemm_kernel(
   }
 }
 
+// logits[i] = part[0][i] + part[1][i] + ... + part[G-1][i], summed in split
+// order, over the n = T * E logits (4 per thread when n allows).
+__global__ __launch_bounds__(256) void router_reduce_kernel(const float* __restrict__ part, int G, int64_t n,
+                                                            float* __restrict__ logits) {
+  const int64_t i4 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i4 >= n) return;
+  if (n % 4 == 0) {
+    float4 a = *reinterpret_cast<const float4*>(part + i4);
+    for (int g = 1; g < G; ++g) {
+      const float4 b = *reinterpret_cast<const float4*>(part + (size_t)g * n + i4);
+      a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+    }
+    *reinterpret_cast<float4*>(logits + i4) = a;
+  } else {
+    for (int64_t i = i4; i < min(n, i4 + 4); ++i) {
+      float a = part[i];
+      for (int g = 1; g < G; ++g) a += part[(size_t)g * n + i];
+      logits[i] = a;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
@@ -337,17 +321,16 @@ static RouterPlan router_plan_cfg(int cfg, int64_t T, int64_t H, int64_t E) {
   p.NT = (int)((E + Cfg::BN - 1) / Cfg::BN);
   p.tiles = (T + Cfg::BM - 1) / Cfg::BM * p.NT;
   // Split H when the tiles alone leave most CUs idle, keeping at least
-  // kRouterMinSplitK per split so the partial tiles stay small next to
-  // the operands, and the counters inside the workspace control block.
+  // kRouterMinSplitK per split so the partial logits stay small next to
+  // the operands.
   int64_t G = 1;
   const int64_t want = 256;
-  if (p.tiles < want && p.tiles <= (int64_t)(kWsCtlBytes / sizeof(uint32_t)))
-    G = std::max<int64_t>(1, std::min<int64_t>(want / p.tiles, H / kRouterMinSplitK));
+  if (p.tiles < want) G = std::max<int64_t>(1, std::min<int64_t>(want / p.tiles, H / kRouterMinSplitK));
   int64_t kchunk = (H + G - 1) / G;
   kchunk = (kchunk + Cfg::BK - 1) / Cfg::BK * Cfg::BK;
   p.G = (int)((H + kchunk - 1) / kchunk);
   p.kchunk = kchunk;
-  p.part_floats = p.G > 1 ? (size_t)p.tiles * p.G * RouterLayout<Cfg>::TILE_FLOATS : 0;
+  p.part_floats = p.G > 1 ? (size_t)p.G * T * E : 0;
   return p;
 }
 
@@ -356,11 +339,12 @@ static RouterPlan router_plan(int64_t T, int64_t H, int64_t E) {
                                : router_plan_cfg<CfgRouter256>(1, T, H, E);
 }
 
-// Bytes of the split-H partial tiles, then (split plans only) the [T, E]
-// fp32 logits that the fused entry point hands to the selection kernel.
+// Bytes of the split-H partial logits [G][T][E] (split plans only).
 static size_t router_part_bytes(const RouterPlan& p) { return (p.part_floats * sizeof(float) + 255) & ~(size_t)255; }
 static size_t router_ws_bytes(const RouterPlan& p, int64_t T, int64_t E) {
-  return kWsCtlBytes + router_part_bytes(p) + (p.G > 1 ? (size_t)T * E * sizeof(float) : 0);
+  (void)T;
+  (void)E;
+  return kWsCtlBytes + router_part_bytes(p);
 }
 
 template <typename T, typename Cfg, int EPI, typename IdxT>
@@ -372,11 +356,10 @@ static int launch_router(const RouterPlan& p, const uint16_t* x, const uint16_t*
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cfg::LDS_BYTES));
     attr_set = true;
   }
-  uint32_t* counters = static_cast<uint32_t*>(ws);
   float* part = p.G > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kWsCtlBytes) : nullptr;
   const int64_t grid = p.tiles * p.G;
   router_gemm_kernel<T, Cfg, EPI, IdxT><<<dim3((unsigned)grid), Cfg::THREADS, Cfg::LDS_BYTES, st>>>(
-      x, wt, Tn, H, E, K, p.NT, p.G, p.kchunk, logits, scores, idx, part, counters);
+      x, wt, Tn, H, E, K, p.NT, p.G, p.kchunk, logits, scores, idx, part);
   return check_launch("router_gemm_kernel");
 }
 
@@ -438,8 +421,16 @@ extern "C" int moe_router_gemm(const void* X, const void* Wt, int dtype, int64_t
   if (int rc = router_check("router_gemm", X, Wt, dtype, T, H, E, workspace, ws_bytes, p)) return rc;
   if (T == 0) return MOE_OK;
   if (!logits) return fail(MOE_EINVAL, "router_gemm: null pointer");
-  return dispatch_router<0, int32_t>(dtype, p, X, Wt, T, H, E, 0, logits, nullptr, nullptr, workspace,
-                                     static_cast<hipStream_t>(stream));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (int rc = dispatch_router<0, int32_t>(dtype, p, X, Wt, T, H, E, 0, logits, nullptr, nullptr, workspace, st))
+    return rc;
+  if (p.G > 1) {
+    const float* part = reinterpret_cast<const float*>(static_cast<char*>(workspace) + kWsCtlBytes);
+    const int64_t n = T * E;
+    router_reduce_kernel<<<(unsigned)((n + 1023) / 1024), 256, 0, st>>>(part, p.G, n, logits);
+    return check_launch("router_reduce_kernel");
+  }
+  return MOE_OK;
 }
 
 extern "C" int moe_router_topk_softmax(const void* X, const void* Wt, int dtype, int64_t T, int64_t H, int64_t E,
@@ -459,14 +450,13 @@ extern "C" int moe_router_topk_softmax(const void* X, const void* Wt, int dtype,
   if (!scores || !indices) return fail(MOE_EINVAL, "router_topk_softmax: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (p.G > 1) {
-    // H is split over G workgroups per tile, which leaves one workgroup per
-    // 64 tokens to run the selection after the reduction: hand the
-    // (L2-resident) logits to the selection kernel instead, one workgroup
-    // per 4 tokens.  Same results as the fused epilogue.
-    float* logits = reinterpret_cast<float*>(static_cast<char*>(workspace) + kWsCtlBytes + router_part_bytes(p));
-    if (int rc = dispatch_router<0, int32_t>(dtype, p, X, Wt, T, H, E, 0, logits, nullptr, nullptr, workspace, st))
+    // H is split over G workgroups per tile: the selection kernel (one wave
+    // per token) sums each token's G partial rows in split order as it loads
+    // them, then selects.  Same results as the fused epilogue.
+    if (int rc = dispatch_router<0, int32_t>(dtype, p, X, Wt, T, H, E, 0, nullptr, nullptr, nullptr, workspace, st))
       return rc;
-    return moe_topk_softmax(logits, MOE_F32, T, E, E, K, scores, indices, idx_dtype, MOE_TOPK_AUTO, nullptr, 0, st);
+    const float* part = reinterpret_cast<const float*>(static_cast<char*>(workspace) + kWsCtlBytes);
+    return topk_select_partials(part, p.G, T, (int)E, (int)K, scores, indices, idx_dtype, st);
   }
   if (idx_dtype == MOE_I64)
     return dispatch_router<1, int64_t>(dtype, p, X, Wt, T, H, E, K, nullptr, scores, static_cast<int64_t*>(indices),
