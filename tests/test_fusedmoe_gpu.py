@@ -106,8 +106,10 @@ def check_routing(x, router_weight, k, wts, ids):
     np.testing.assert_allclose(wts.double().cpu().numpy(), p, rtol=1e-4, atol=1e-7)
 
 
+# Ds == De: the shared expert rides in the routed grouped GEMMs as expert E;
+# Ds == 2 De (two shared experts): separate shared GEMMs.
 @pytest.mark.parametrize("T,Dh,De,Ds,E,k", [(64, 256, 128, 128, 8, 2), (200, 512, 256, 0, 16, 4),
-                                            (33, 1024, 512, 512, 4, 4)])
+                                            (33, 1024, 512, 512, 4, 4), (48, 256, 128, 256, 8, 2)])
 def test_fusedmoe_vs_numpy_oracle(cuda, T, Dh, De, Ds, E, k):
     x, w = _moe_weights(T, Dh, De, Ds, E, seed=T + E)
     out, wts, ids = K.fused_moe_routed(x, **w, n_experts_per_token=k, return_routing=True)
@@ -138,7 +140,11 @@ def torch_moe_ref(x, w, k, wts, ids):
     return out
 
 
-@pytest.mark.parametrize("T,Dh,De,Ds,E,k", [(2048, 2048, 1024, 1024, 8, 4), (4096, 1024, 512, 0, 64, 6)])
+# (4096, 4096, 256, 256, 8, 2): the up GEMM takes 64-row tiles and the down
+# GEMM 256-row tiles, so the down GEMM rebuilds the tile table from the up
+# GEMM's routing.
+@pytest.mark.parametrize("T,Dh,De,Ds,E,k", [(2048, 2048, 1024, 1024, 8, 4), (4096, 1024, 512, 0, 64, 6),
+                                            (4096, 4096, 256, 256, 8, 2)])
 def test_fusedmoe_large(cuda, T, Dh, De, Ds, E, k):
     x, w = _moe_weights(T, Dh, De, Ds, E, seed=T)
     out, wts, ids = K.fused_moe_routed(x, **w, n_experts_per_token=k, return_routing=True)

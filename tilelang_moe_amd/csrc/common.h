@@ -31,6 +31,24 @@ int check_launch(const char* what);
 int topk_select_partials(const float* part, int G, int64_t M, int N, int K, float* scores, void* indices,
                          int idx_dtype, hipStream_t st);
 
+// Grouped GEMM with an appended expert and reusable routing tables, for
+// the FusedMoE path (defined with the grouped GEMM, gemm.hip).  Rows
+// T*topk .. T*topk + Tx - 1 form expert E, with weights Wx (and W2x for the
+// SwiGLU epilogue) and X row r - T*topk + x_shift.  reuse_bm = 0 sorts the
+// rows; reuse_bm = b > 0 reuses the routing tables an earlier call on the
+// same workspace built for the same rows with tile height b (bm_used).
+struct GemmExtra {
+  const void* Wx = nullptr;
+  const void* W2x = nullptr;
+  int64_t Tx = 0;
+  int64_t x_shift = 0;
+  int reuse_bm = 0;
+};
+size_t grouped_gemm_ws_bytes(int64_t R, int64_t E);
+int grouped_gemm_run(int epi, const void* X, const void* W, const void* W2, const void* expert_ids, int dtype,
+                     int idx_dtype, int64_t T, int64_t topk, int64_t H, int64_t I, int64_t E, const GemmExtra& ex,
+                     void* Y, void* workspace, size_t ws_bytes, hipStream_t stream, int* bm_used);
+
 constexpr int kWave = 64;
 // Every workspace starts with a control block of this size: the only bytes
 // that must be zero before a call, and every call leaves them zero.  Scratch

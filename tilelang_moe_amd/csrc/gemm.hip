@@ -28,9 +28,15 @@ constexpr int kRouteThreads = 256;
 constexpr int kMaxExperts = 4096;
 constexpr int kScanThreads = 1024;
 
+// Bucket of routed row r.  Rows r < R_ids carry an expert id, valid in
+// [0, E_ids); rows r >= R_ids (an appended set, e.g. a shared expert taken
+// by every token) belong to expert E_ids.  Bucket E (the number of experts,
+// E_ids or E_ids + 1) collects the invalid ids.
 template <typename IdxT>
-__device__ inline int bucket_of(IdxT v, int E) {
-  return (v >= 0 && v < (IdxT)E) ? (int)v : E;
+__device__ inline int bucket_of(const IdxT* ids, int64_t r, int64_t R_ids, int E_ids, int E) {
+  if (r >= R_ids) return E_ids;
+  const IdxT v = ids[r];
+  return (v >= 0 && v < (IdxT)E_ids) ? (int)v : E;
 }
 
 // ---------------------------------------------------------------------------
@@ -38,17 +44,18 @@ __device__ inline int bucket_of(IdxT v, int E) {
 // Rows are cut into chunks of `chunk` rows; blockcnt is laid out expert-major
 // ([E+1][nb]) so that one exclusive scan over it yields, for every (expert,
 // chunk), where that chunk's rows of that expert start in sorted_rows.
-// Bucket E collects rows whose id is outside [0, E).
+// Bucket E collects rows whose id is invalid (bucket_of).
 // ---------------------------------------------------------------------------
 template <typename IdxT>
 __global__ __launch_bounds__(kRouteThreads) void route_count_kernel(
-    const IdxT* __restrict__ ids, int64_t R, int E, int chunk, int nb, int32_t* __restrict__ blockcnt) {
+    const IdxT* __restrict__ ids, int64_t R, int64_t R_ids, int E_ids, int E, int chunk, int nb,
+    int32_t* __restrict__ blockcnt) {
   extern __shared__ int32_t hist[];  // [E+1]
   for (int e = threadIdx.x; e <= E; e += kRouteThreads) hist[e] = 0;
   __syncthreads();
   const int64_t lo = (int64_t)blockIdx.x * chunk;
   const int64_t hi = std::min<int64_t>(R, lo + chunk);
-  for (int64_t r = lo + threadIdx.x; r < hi; r += kRouteThreads) atomicAdd(&hist[bucket_of(ids[r], E)], 1);
+  for (int64_t r = lo + threadIdx.x; r < hi; r += kRouteThreads) atomicAdd(&hist[bucket_of(ids, r, R_ids, E_ids, E)], 1);
   __syncthreads();
   for (int e = threadIdx.x; e <= E; e += kRouteThreads) blockcnt[(int64_t)e * nb + blockIdx.x] = hist[e];
 }
@@ -65,6 +72,10 @@ __device__ inline int32_t block_excl_scan(int32_t v, int32_t* wsum) {
   __syncthreads();
   return base + incl - v;
 }
+
+__device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int32_t* wsum,
+                                        int32_t* __restrict__ tile_expert, int32_t* __restrict__ tile_mstart,
+                                        int32_t* __restrict__ meta);
 
 // Single workgroup.  In: blockcnt ([E+1][nb] counts, nb <= 64).  Out:
 // blockcnt[e][b] = rows of expert e in chunks before b (one wave scans one
@@ -117,8 +128,16 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     if (e < E) counts[e] = s_off[e + 1] - s_off[e];
   }
   if (bm <= 0) return;
+  build_tile_table(s_off, E, bm, wsum, tile_expert, tile_mstart, meta);
+}
 
-  // Tile table: expert e owns ceil(count_e / bm) consecutive M tiles.
+// The M-tile table for tile height bm from segment offsets already in LDS
+// (s_off[0..E], published by a barrier): expert e owns ceil(count_e / bm)
+// consecutive M tiles; meta[0] = number of tiles.  One 1024-thread block.
+__device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int32_t* wsum,
+                                        int32_t* __restrict__ tile_expert, int32_t* __restrict__ tile_mstart,
+                                        int32_t* __restrict__ meta) {
+  const int tid = threadIdx.x;
   const int perE = (E + kScanThreads - 1) / kScanThreads;
   const int elo = std::min(E, tid * perE), ehi = std::min(E, elo + perE);
   int32_t nt = 0;
@@ -134,9 +153,22 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
   if (ehi == E && elo < ehi) meta[0] = t;  // the thread owning the last expert
 }
 
+// The tile table alone, for routing tables built by an earlier call for a
+// different tile height (offsets[0..E] are final).
+__global__ __launch_bounds__(kScanThreads) void route_tiles_kernel(const int32_t* __restrict__ offsets, int E, int bm,
+                                                                  int32_t* __restrict__ tile_expert,
+                                                                  int32_t* __restrict__ tile_mstart,
+                                                                  int32_t* __restrict__ meta) {
+  __shared__ int32_t wsum[kScanThreads / kWave];
+  __shared__ int32_t s_off[kMaxExperts + 2];
+  for (int e = threadIdx.x; e <= E; e += kScanThreads) s_off[e] = offsets[e];
+  __syncthreads();
+  build_tile_table(s_off, E, bm, wsum, tile_expert, tile_mstart, meta);
+}
+
 template <typename IdxT>
 __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
-    const IdxT* __restrict__ ids, int64_t R, int E, int chunk, int nb,
+    const IdxT* __restrict__ ids, int64_t R, int64_t R_ids, int E_ids, int E, int chunk, int nb,
     const int32_t* __restrict__ blockoff, const int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_rows) {
   extern __shared__ int32_t sm[];  // base[E+1], wcnt[4][E+1]
@@ -154,7 +186,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
     __syncthreads();
     const int64_t r = sub + tid;
     const bool valid = r < hi;
-    const int e = valid ? bucket_of(ids[r], E) : 0;
+    const int e = valid ? bucket_of(ids, r, R_ids, E_ids, E) : 0;
     // Lanes holding the same bucket: intersect the ballots of every bit.
     uint64_t match = __ballot(valid);
     for (int b = 0; b < nbits; ++b) {
@@ -195,8 +227,8 @@ using CfgSmall = GemmCfg<64, 128, 2, 2, 64, 3>;      // 4 waves of 32x64,   72 K
 template <typename T, typename Cfg, int MODE = 0, int EPI = 0>  // MODE: tuning builds only (1 = copies only, 2 = MFMA only)
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
     const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
-    uint16_t* __restrict__ Y,
-    int64_t H, int64_t I, int topk, int64_t R, int E, int ntn,
+    const uint16_t* __restrict__ Wx, const uint16_t* __restrict__ W2x, uint16_t* __restrict__ Y,
+    int64_t H, int64_t I, int topk, int64_t R, int E, int ntn, int64_t R_ids, int E_ids, int64_t x_shift,
     const int32_t* __restrict__ sorted_rows, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_mstart,
     const int32_t* __restrict__ meta) {
@@ -272,6 +304,11 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
   const int m0 = tile_mstart[mt];
   const int mend = offsets[e + 1];
   for (int r = tid; r < BM; r += Cfg::THREADS) srow[r] = (m0 + r < mend) ? sorted_rows[m0 + r] : -1;
+  // Expert e < E_ids reads W[e] (and W2[e]); the appended expert E_ids reads
+  // Wx (and W2x).  X row of routed row r: r / topk for r < R_ids, else
+  // r - R_ids + x_shift.
+  const uint16_t* We = e < E_ids ? W + (int64_t)e * I * H : Wx;
+  const uint16_t* W2e = e < E_ids ? W2 + (int64_t)e * I * H : W2x;
   __syncthreads();
 
   // Copy plan: instruction i of wave v covers tile rows RPI*(v*INS + i) ..;
@@ -284,19 +321,20 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
   for (int i = 0; i < Cfg::A_INS; ++i) {
     const int r = Cfg::RPI * (wave * Cfg::A_INS + i) + crow;
     const int sr = srow[r];
-    // Rows past the expert's segment read token 0; their results are never stored.
-    a_src[i] = X + (int64_t)(sr >= 0 ? sr / topk : 0) * H + cchunk * 8;
+    // Rows past the expert's segment read X row 0; their results are never stored.
+    const int64_t xr = sr < 0 ? 0 : (sr < R_ids ? sr / topk : sr - R_ids + x_shift);
+    a_src[i] = X + xr * H + cchunk * 8;
   }
 #pragma unroll
   for (int i = 0; i < Cfg::B_INS; ++i) {
     const int nl = Cfg::RPI * (wave * Cfg::B_INS + i) + crow;  // tile row
     if constexpr (EPI == 0) {
       const int64_t n = n0 + nl;
-      b_src[i] = W + ((int64_t)e * I + (n < I ? n : 0)) * H + cchunk * 8;
+      b_src[i] = We + (n < I ? n : 0) * H + cchunk * 8;
     } else {
       const int blk = nl / 32;
       const int64_t n = n0 + (blk >> 1) * 32 + (nl & 31);
-      b_src[i] = ((blk & 1) ? W2 : W) + ((int64_t)e * I + (n < I ? n : 0)) * H + cchunk * 8;
+      b_src[i] = ((blk & 1) ? W2e : We) + (n < I ? n : 0) * H + cchunk * 8;
     }
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
@@ -394,13 +432,15 @@ static GemmLayout gemm_layout(int64_t R, int64_t E) {
   return g;
 }
 
+// Rows r < R_ids carry ids valid in [0, E_ids); rows R_ids .. R-1 belong to
+// expert E_ids (E = E_ids + 1 then, else E = E_ids).
 template <typename IdxT>
-static int launch_route(const IdxT* ids, int64_t R, int E, int32_t* blockcnt, int32_t* counts,
-                        int32_t* offsets, int32_t* sorted_rows, int bm, int32_t* tile_expert,
+static int launch_route(const IdxT* ids, int64_t R, int64_t R_ids, int E_ids, int E, int32_t* blockcnt,
+                        int32_t* counts, int32_t* offsets, int32_t* sorted_rows, int bm, int32_t* tile_expert,
                         int32_t* tile_mstart, int32_t* meta, hipStream_t st) {
   const RoutePlan p = route_plan(R);
   const size_t hist_lds = (size_t)(E + 1) * sizeof(int32_t);
-  route_count_kernel<IdxT><<<p.nb, kRouteThreads, hist_lds, st>>>(ids, R, E, p.chunk, p.nb, blockcnt);
+  route_count_kernel<IdxT><<<p.nb, kRouteThreads, hist_lds, st>>>(ids, R, R_ids, E_ids, E, p.chunk, p.nb, blockcnt);
   if (int rc = check_launch("route_count_kernel")) return rc;
   route_scan_kernel<<<1, kScanThreads, 0, st>>>(blockcnt, R, E, p.nb, counts, offsets, bm, tile_expert,
                                                  tile_mstart, meta);
@@ -413,15 +453,16 @@ static int launch_route(const IdxT* ids, int64_t R, int E, int32_t* blockcnt, in
                                       (int)((kMaxExperts + 1) * (1 + kRouteThreads / kWave) * sizeof(int32_t))));
     attr_set = true;
   }
-  route_scatter_kernel<IdxT><<<p.nb, kRouteThreads, scat_lds, st>>>(ids, R, E, p.chunk, p.nb, blockcnt,
-                                                                     offsets, sorted_rows);
+  route_scatter_kernel<IdxT><<<p.nb, kRouteThreads, scat_lds, st>>>(ids, R, R_ids, E_ids, E, p.chunk, p.nb,
+                                                                     blockcnt, offsets, sorted_rows);
   return check_launch("route_scatter_kernel");
 }
 
 template <typename T, typename Cfg, int MODE = 0, int EPI = 0>
-static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, const uint16_t* w2, uint16_t* y,
-                       int64_t H, int64_t I, int topk, int64_t R, int E, int ntn, const int32_t* sorted,
-                       const int32_t* offsets, const int32_t* t_exp, const int32_t* t_ms, const int32_t* meta) {
+static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, const uint16_t* w2, const uint16_t* wx,
+                       const uint16_t* w2x, uint16_t* y, int64_t H, int64_t I, int topk, int64_t R, int E, int ntn,
+                       int64_t R_ids, int E_ids, int64_t x_shift, const int32_t* sorted, const int32_t* offsets,
+                       const int32_t* t_exp, const int32_t* t_ms, const int32_t* meta) {
   static bool attr_set = false;
   if (!attr_set) {
     MOE_HIP_CHECK(hipFuncSetAttribute((const void*)grouped_gemm_kernel<T, Cfg, MODE, EPI>,
@@ -433,7 +474,7 @@ static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, con
   const int64_t ub = ((R + Cfg::BM - 1) / Cfg::BM + E + 1) * ntn;  // tiles, upper bound
   const int64_t grid = ub >= 16 * Cfg::SUPER ? 8 * Cfg::SUPER : (ub + 7) / 8 * 8;
   grouped_gemm_kernel<T, Cfg, MODE, EPI><<<dim3((unsigned)grid), Cfg::THREADS, Cfg::LDS_BYTES, st>>>(
-      x, w, w2, y, H, I, topk, R, E, ntn, sorted, offsets, t_exp, t_ms, meta);
+      x, w, w2, wx, w2x, y, H, I, topk, R, E, ntn, R_ids, E_ids, x_shift, sorted, offsets, t_exp, t_ms, meta);
   return MOE_OK;
 }
 
@@ -462,9 +503,9 @@ extern "C" int moe_route_sort(const void* expert_ids, int idx_dtype, int64_t R, 
   hipStream_t st = static_cast<hipStream_t>(stream);
   int32_t* blockcnt = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + kWsCtlBytes);
   if (idx_dtype == MOE_I64)
-    return launch_route(static_cast<const int64_t*>(expert_ids), R, (int)E, blockcnt, counts, offsets,
+    return launch_route(static_cast<const int64_t*>(expert_ids), R, R, (int)E, (int)E, blockcnt, counts, offsets,
                         sorted_rows, 0, nullptr, nullptr, nullptr, st);
-  return launch_route(static_cast<const int32_t*>(expert_ids), R, (int)E, blockcnt, counts, offsets,
+  return launch_route(static_cast<const int32_t*>(expert_ids), R, R, (int)E, (int)E, blockcnt, counts, offsets,
                       sorted_rows, 0, nullptr, nullptr, nullptr, st);
 }
 
@@ -476,28 +517,37 @@ extern "C" size_t moe_grouped_gemm_workspace_size(int64_t T, int64_t topk, int64
 
 namespace moe {
 
-// Shared by moe_grouped_gemm (EPI 0) and moe_grouped_gemm_swiglu (EPI 1,
-// W2 = the up weights; I is the output width, the tile rows cover 2 I).
+size_t grouped_gemm_ws_bytes(int64_t R, int64_t E) { return kWsCtlBytes + gemm_layout(R, E).total; }
+
+// Shared by moe_grouped_gemm (EPI 0), moe_grouped_gemm_swiglu (EPI 1,
+// W2 = the up weights; I is the output width, the tile rows cover 2 I) and,
+// through grouped_gemm_run, the FusedMoE path (an appended expert, routing
+// tables reused across calls).
 template <int EPI>
 static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const void* W2, const void* expert_ids,
                              int dtype, int idx_dtype, int64_t T, int64_t topk, int64_t H, int64_t I, int64_t E,
-                             void* Y, void* workspace, size_t ws_bytes, void* stream) {
+                             const GemmExtra& ex, void* Y, void* workspace, size_t ws_bytes, void* stream,
+                             int* bm_used) {
   const std::string f(fn);
-  if (T < 0 || topk < 1 || H < 1 || I < 1) return fail(MOE_EINVAL, f + ": need T >= 0, topk >= 1, H >= 1, I >= 1");
-  if (E < 1 || E > kMaxExperts) return fail(MOE_EUNSUP, f + ": need 1 <= E <= 4096");
+  if (T < 0 || topk < 1 || H < 1 || I < 1 || ex.Tx < 0) return fail(MOE_EINVAL, f + ": need T >= 0, topk >= 1, H >= 1, I >= 1");
+  if (E < 1 || E + (ex.Tx > 0) > kMaxExperts) return fail(MOE_EUNSUP, f + ": need 1 <= E <= 4096");
   if (H % 8 != 0) return fail(MOE_EUNSUP, f + ": H must be a multiple of 8");
-  const int64_t R = T * topk;
+  const int64_t R_ids = T * topk;
+  const int64_t R = R_ids + ex.Tx;
+  const int64_t Et = E + (ex.Tx > 0 ? 1 : 0);  // the appended rows form expert E
   const int64_t Iv = EPI == 1 ? 2 * I : I;  // weight rows per expert the tiles walk
-  if (R >= INT32_MAX || (R + kMinBM - 1) / kMinBM + E + 1 > (int64_t)INT32_MAX / ((Iv + 63) / 64))
+  if (R >= INT32_MAX || (R + kMinBM - 1) / kMinBM + Et + 1 > (int64_t)INT32_MAX / ((Iv + 63) / 64))
     return fail(MOE_EUNSUP, f + ": problem too large");
   if (dtype != MOE_BF16 && dtype != MOE_F16)
     return fail(MOE_EINVAL, f + ": X, W and Y must be bfloat16 or float16");
   if (idx_dtype != MOE_I32 && idx_dtype != MOE_I64) return fail(MOE_EINVAL, f + ": expert ids must be int32 or int64");
   if (R == 0) return MOE_OK;
-  if (!X || !W || !expert_ids || !Y || (EPI == 1 && !W2)) return fail(MOE_EINVAL, f + ": null pointer");
-  if (((uintptr_t)X | (uintptr_t)W | (uintptr_t)W2) & 15)
+  if (!X || !W || (R_ids > 0 && !expert_ids) || !Y || (EPI == 1 && !W2) ||
+      (ex.Tx > 0 && (!ex.Wx || (EPI == 1 && !ex.W2x))))
+    return fail(MOE_EINVAL, f + ": null pointer");
+  if (((uintptr_t)X | (uintptr_t)W | (uintptr_t)W2 | (uintptr_t)ex.Wx | (uintptr_t)ex.W2x) & 15)
     return fail(MOE_EINVAL, f + ": X and the weights must be 16-byte aligned");
-  const GemmLayout g = gemm_layout(R, E);
+  const GemmLayout g = gemm_layout(R, Et);
   if (!workspace || ws_bytes < kWsCtlBytes + g.total)
     return fail(MOE_EINVAL, f + ": workspace too small (" + std::to_string(ws_bytes) + " < " +
                                 std::to_string(kWsCtlBytes + g.total) + ")");
@@ -517,31 +567,48 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   const int cfg = tiles_of(CfgHuge::BM, CfgHuge::BN) >= 512 ? 2 : tiles_of(CfgLarge::BM, CfgLarge::BN) >= 512 ? 1 : 0;
   const int bm = cfg == 2 ? CfgHuge::BM : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
   const int bn = cfg == 2 ? CfgHuge::BN : cfg == 1 ? CfgLarge::BN : CfgSmall::BN;
-  int rc;
-  if (idx_dtype == MOE_I64)
-    rc = launch_route(static_cast<const int64_t*>(expert_ids), R, (int)E, blockcnt, counts, offsets, sorted,
-                      bm, t_exp, t_ms, meta, st);
-  else
-    rc = launch_route(static_cast<const int32_t*>(expert_ids), R, (int)E, blockcnt, counts, offsets, sorted,
-                      bm, t_exp, t_ms, meta, st);
+  if (bm_used) *bm_used = bm;
+  int rc = MOE_OK;
+  if (ex.reuse_bm == 0) {
+    if (idx_dtype == MOE_I64)
+      rc = launch_route(static_cast<const int64_t*>(expert_ids), R, R_ids, (int)E, (int)Et, blockcnt, counts, offsets,
+                        sorted, bm, t_exp, t_ms, meta, st);
+    else
+      rc = launch_route(static_cast<const int32_t*>(expert_ids), R, R_ids, (int)E, (int)Et, blockcnt, counts, offsets,
+                        sorted, bm, t_exp, t_ms, meta, st);
+  } else if (ex.reuse_bm != bm) {
+    route_tiles_kernel<<<1, kScanThreads, 0, st>>>(offsets, (int)Et, bm, t_exp, t_ms, meta);
+    rc = check_launch("route_tiles_kernel");
+  }
   if (rc) return rc;
   const int obn = EPI == 1 ? bn / 2 : bn;
   const int ntn = (int)((I + obn - 1) / obn);
   const uint16_t* x = static_cast<const uint16_t*>(X);
   const uint16_t* w = static_cast<const uint16_t*>(W);
   const uint16_t* w2 = static_cast<const uint16_t*>(W2);
+  const uint16_t* wx = static_cast<const uint16_t*>(ex.Wx);
+  const uint16_t* w2x = static_cast<const uint16_t*>(ex.W2x);
   uint16_t* y = static_cast<uint16_t*>(Y);
   auto run = [&](auto cfg_tag) {
     using C = decltype(cfg_tag);
     return dtype == MOE_BF16
-               ? launch_gemm<uint16_t, C, 0, EPI>(st, x, w, w2, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets,
-                                                 t_exp, t_ms, meta)
-               : launch_gemm<Half16, C, 0, EPI>(st, x, w, w2, y, H, I, (int)topk, R, (int)E, ntn, sorted, offsets,
-                                               t_exp, t_ms, meta);
+               ? launch_gemm<uint16_t, C, 0, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn, R_ids,
+                                                 (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta)
+               : launch_gemm<Half16, C, 0, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn, R_ids,
+                                               (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta);
   };
   rc = cfg == 2 ? run(CfgHuge{}) : cfg == 1 ? run(CfgLarge{}) : run(CfgSmall{});
   if (rc) return rc;
   return check_launch("grouped_gemm_kernel");
+}
+
+int grouped_gemm_run(int epi, const void* X, const void* W, const void* W2, const void* expert_ids, int dtype,
+                     int idx_dtype, int64_t T, int64_t topk, int64_t H, int64_t I, int64_t E, const GemmExtra& ex,
+                     void* Y, void* workspace, size_t ws_bytes, hipStream_t stream, int* bm_used) {
+  return epi == 1 ? grouped_gemm_impl<1>("grouped_gemm_swiglu", X, W, W2, expert_ids, dtype, idx_dtype, T, topk, H,
+                                         I, E, ex, Y, workspace, ws_bytes, stream, bm_used)
+                  : grouped_gemm_impl<0>("grouped_gemm", X, W, nullptr, expert_ids, dtype, idx_dtype, T, topk, H, I,
+                                         E, ex, Y, workspace, ws_bytes, stream, bm_used);
 }
 
 }  // namespace moe
@@ -549,14 +616,14 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
 extern "C" int moe_grouped_gemm(const void* X, const void* W, const void* expert_ids, int dtype,
                                 int idx_dtype, int64_t T, int64_t topk, int64_t H, int64_t I,
                                 int64_t E, void* Y, void* workspace, size_t ws_bytes, void* stream) {
-  return grouped_gemm_impl<0>("grouped_gemm", X, W, nullptr, expert_ids, dtype, idx_dtype, T, topk, H, I, E, Y,
-                              workspace, ws_bytes, stream);
+  return grouped_gemm_impl<0>("grouped_gemm", X, W, nullptr, expert_ids, dtype, idx_dtype, T, topk, H, I, E,
+                              GemmExtra{}, Y, workspace, ws_bytes, stream, nullptr);
 }
 
 extern "C" int moe_grouped_gemm_swiglu(const void* X, const void* Wg, const void* Wu, const void* expert_ids,
                                        int dtype, int idx_dtype, int64_t T, int64_t topk, int64_t H,
                                        int64_t I, int64_t E, void* Y, void* workspace, size_t ws_bytes,
                                        void* stream) {
-  return grouped_gemm_impl<1>("grouped_gemm_swiglu", X, Wg, Wu, expert_ids, dtype, idx_dtype, T, topk, H, I, E, Y,
-                              workspace, ws_bytes, stream);
+  return grouped_gemm_impl<1>("grouped_gemm_swiglu", X, Wg, Wu, expert_ids, dtype, idx_dtype, T, topk, H, I, E,
+                              GemmExtra{}, Y, workspace, ws_bytes, stream, nullptr);
 }

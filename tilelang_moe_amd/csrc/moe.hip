@@ -5,10 +5,16 @@
 //
 //   logits = x . router_w^T                    moe_router_gemm (fp32)
 //   w, idx = top-k of softmax(logits)          moe_topk_softmax_ex, Convention A
-//   h      = silu(x Wg[e]^T) * (x Wu[e]^T)     moe_grouped_gemm_swiglu, per routed row
-//   y      = h Wd[e]^T                         moe_grouped_gemm
-//   hs, ys = the same for the shared expert    one-expert grouped GEMMs over all tokens
+//   h      = silu(x Wg[e]^T) * (x Wu[e]^T)     SwiGLU grouped GEMM, per routed row
+//   y      = h Wd[e]^T                         grouped GEMM
+//   hs, ys = the same for the shared expert
 //   out[t] = ys[t] + sum_j w[t,j] y[t k + j]   moe_combine_kernel (fp32, fixed order)
+//
+// When the shared expert is as wide as a routed one (Ds == De) it is
+// expert E of the same grouped GEMMs: T more rows, one per token, appended
+// after the T k routed rows, with their own weight pointers; the down GEMM
+// reuses the up GEMM's routing tables.  A forward is then the router GEMM,
+// the top-k, one routing sort, two grouped GEMMs and the combine.
 //
 // Every step is a stream-ordered kernel; there is no host synchronisation,
 // no per-expert loop and no scatter_reduce (the combine reads each token's
@@ -81,26 +87,35 @@ struct MoeLayout {
 
 static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// The shared expert rides in the routed grouped GEMMs as expert E.
+static bool moe_merged_shared(int64_t De, int64_t Ds) { return Ds > 0 && Ds == De; }
+
 static MoeLayout moe_layout(int64_t T, int64_t Dh, int64_t De, int64_t Ds, int64_t E, int64_t k) {
   MoeLayout L;
   const size_t ctl = kWsCtlBytes;
+  const bool merged = moe_merged_shared(De, Ds);
+  const int64_t rows = T * k + (merged ? T : 0);  // rows of h and y
   size_t scratch = 0;
   auto take = [&](size_t ws) { scratch = std::max(scratch, ws > ctl ? ws - ctl : 0); };
   take(moe_router_workspace_size(T, Dh, E));
   take(moe_topk_softmax_workspace_size(T, E, k, MOE_TOPK_AUTO));
-  take(moe_grouped_gemm_workspace_size(T, k, E, std::max(De, Dh)));
-  take(moe_grouped_gemm_workspace_size(T * k, 1, E, Dh));
-  if (Ds > 0) take(moe_grouped_gemm_workspace_size(T, 1, 1, std::max(Ds, Dh)));
+  if (merged) {
+    take(grouped_gemm_ws_bytes(rows, E + 1));
+  } else {
+    take(moe_grouped_gemm_workspace_size(T, k, E, std::max(De, Dh)));
+    take(moe_grouped_gemm_workspace_size(T * k, 1, E, Dh));
+    if (Ds > 0) take(moe_grouped_gemm_workspace_size(T, 1, 1, std::max(Ds, Dh)));
+  }
   L.scratch = up256(scratch);
   size_t o = ctl + L.scratch;
   L.logits = o; o += up256((size_t)T * E * 4);
   L.w = o; o += up256((size_t)T * k * 4);
   L.idx = o; o += up256((size_t)T * k * 4);
-  L.zeros = o; o += up256((size_t)T * 4);
-  L.h = o; o += up256((size_t)T * k * De * 2);
-  L.y = o; o += up256((size_t)T * k * Dh * 2);
-  L.hs = o; o += up256((size_t)T * std::max<int64_t>(Ds, 0) * 2);
-  L.ys = o; o += up256((size_t)T * (Ds > 0 ? Dh : 0) * 2);
+  L.zeros = o; o += up256(merged ? 0 : (size_t)T * 4);
+  L.h = o; o += up256((size_t)rows * De * 2);
+  L.y = o; o += up256((size_t)rows * Dh * 2);
+  L.hs = o; o += up256(merged ? 0 : (size_t)T * std::max<int64_t>(Ds, 0) * 2);
+  L.ys = o; o += up256(merged ? 0 : (size_t)T * (Ds > 0 ? Dh : 0) * 2);
   L.total = o;
   return L;
 }
@@ -172,6 +187,29 @@ extern "C" int moe_fused_moe(const void* x, const void* router_w, const void* sh
   if ((rc = moe_topk_softmax_ex(logits, MOE_F32, T, E, E, k, w, idx, MOE_I32, MOE_TOPK_AUTO, MOE_SCORES_ALL, ws,
                                 sub, stream)))
     return rc;
+  if (moe_merged_shared(De, Ds)) {
+    // 2. Routed experts and the shared one (expert E, rows T k .. T k + T - 1
+    //    = tokens 0 .. T - 1): gate/up with the SwiGLU epilogue, then down
+    //    over the same routing tables (h row r is the down GEMM's X row r).
+    GemmExtra up;
+    up.Wx = shared_gate;
+    up.W2x = shared_up;
+    up.Tx = T;
+    int bm = 0;
+    if ((rc = grouped_gemm_run(1, x, routed_gate, routed_up, idx, dtype, MOE_I32, T, k, Dh, De, E, up, h, ws, sub, st,
+                               &bm)))
+      return rc;
+    GemmExtra down;
+    down.Wx = shared_down;
+    down.Tx = T;
+    down.x_shift = T * k;
+    down.reuse_bm = bm;
+    if ((rc = grouped_gemm_run(0, h, routed_down, nullptr, idx, dtype, MOE_I32, T * k, 1, De, Dh, E, down, y, ws, sub,
+                               st, nullptr)))
+      return rc;
+    // 3. Combine: the shared rows follow the routed ones in y.
+    return moe_combine(y, static_cast<char*>(y) + (size_t)T * k * Dh * 2, w, dtype, T, k, Dh, out, stream);
+  }
   // 2. Routed experts: gate/up with the SwiGLU epilogue, then down.
   if ((rc = moe_grouped_gemm_swiglu(x, routed_gate, routed_up, idx, dtype, MOE_I32, T, k, Dh, De, E, h, ws, sub,
                                     stream)))
