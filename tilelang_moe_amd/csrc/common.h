@@ -25,11 +25,19 @@ int check_launch(const char* what);
                                        hipGetErrorString(_e));                 \
   } while (0)
 
-// Top-K + softmax (Convention B) of the rows sum_g part[g][M][N], g in
-// order 0..G-1 (fp32 partials of a split-H router GEMM), N <= 256; one wave
-// per row.  Defined with the selection kernel (router.hip).
-int topk_select_partials(const float* part, int G, int64_t M, int N, int K, float* scores, void* indices,
-                         int idx_dtype, hipStream_t st);
+// Top-K + softmax of the rows sum_g part[g][M][N], g in order 0..G-1 (fp32
+// partials of a split-H router GEMM), N <= 256; one wave per row.
+// score_mode MOE_SCORES_TOPK (Convention B) or MOE_SCORES_ALL (A).
+// Defined with the selection kernel (router.hip).
+int topk_select_partials(const float* part, int G, int64_t M, int N, int K, int score_mode, float* scores,
+                         void* indices, int idx_dtype, hipStream_t st);
+// Router GEMM for the fused paths: the plan's split count G, and either the
+// logits [T, E] (G == 1, written to `logits`) or G partial rows per token
+// (G > 1, returned in *part, inside the workspace).  Defined with the
+// router GEMM (router_gemm.hip).
+int router_gemm_logits_or_partials(const void* X, const void* Wt, int dtype, int64_t T, int64_t H, int64_t E,
+                                   float* logits, const float** part, int* G, void* workspace, size_t ws_bytes,
+                                   hipStream_t st);
 
 // Grouped GEMM with an appended expert and reusable routing tables, for
 // the FusedMoE path (defined with the grouped GEMM, gemm.hip).  Rows

@@ -133,12 +133,12 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
 
 // The M-tile table for tile height bm from segment offsets already in LDS
 // (s_off[0..E], published by a barrier): expert e owns ceil(count_e / bm)
-// consecutive M tiles; meta[0] = number of tiles.  One 1024-thread block.
+// consecutive M tiles; meta[0] = number of tiles.  One block (any size).
 __device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int32_t* wsum,
                                         int32_t* __restrict__ tile_expert, int32_t* __restrict__ tile_mstart,
                                         int32_t* __restrict__ meta) {
   const int tid = threadIdx.x;
-  const int perE = (E + kScanThreads - 1) / kScanThreads;
+  const int perE = (E + (int)blockDim.x - 1) / (int)blockDim.x;
   const int elo = std::min(E, tid * perE), ehi = std::min(E, elo + perE);
   int32_t nt = 0;
   for (int e = elo; e < ehi; ++e) nt += (s_off[e + 1] - s_off[e] + bm - 1) / bm;
@@ -206,6 +206,86 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
       int32_t s = 0;
       for (int w = 0; w < NW; ++w) s += wcnt[w * (E + 1) + b];
       base[b] += s;
+    }
+    __syncthreads();
+  }
+}
+
+// The whole routing sort in one workgroup of kRouteSmallThreads, for small
+// problems (R <= kRouteSmallRows, E <= kRouteSmallE): the histogram, the
+// segment offsets, the tile table (bm > 0) and the stable scatter of
+// route_count / route_scan / route_scatter, without their two launches and
+// the blockcnt round trip.  The scatter takes kRouteSmallThreads rows per
+// round, so it is kept to a few rounds.
+constexpr int kRouteSmallThreads = 1024;
+constexpr int64_t kRouteSmallRows = 4096;
+constexpr int kRouteSmallE = 256;
+
+template <typename IdxT>
+__global__ __launch_bounds__(kRouteSmallThreads) void route_small_kernel(
+    const IdxT* __restrict__ ids, int64_t R, int64_t R_ids, int E_ids, int E, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_rows, int bm, int32_t* __restrict__ tile_expert,
+    int32_t* __restrict__ tile_mstart, int32_t* __restrict__ meta) {
+  constexpr int NW = kRouteSmallThreads / kWave;
+  __shared__ int32_t s_off[kRouteSmallE + 2];     // counts, then segment starts
+  __shared__ int32_t wcnt[NW * (kRouteSmallE + 1)];
+  __shared__ int32_t wsum[NW];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  for (int e = tid; e <= E; e += kRouteSmallThreads) s_off[e] = 0;
+  __syncthreads();
+  for (int64_t r = tid; r < R; r += kRouteSmallThreads) atomicAdd(&s_off[bucket_of(ids, r, R_ids, E_ids, E)], 1);
+  __syncthreads();
+  // Exclusive scan of the E + 1 bucket counts (contiguous runs per thread).
+  const int per = (E + 1 + kRouteSmallThreads - 1) / kRouteSmallThreads;  // 1 for E <= 256
+  const int lo = std::min(E + 1, tid * per), hi = std::min(E + 1, lo + per);
+  int32_t tot[1], sum = 0;
+#pragma unroll
+  for (int q = 0; q < 1; ++q) {
+    tot[q] = (lo + q < hi) ? s_off[lo + q] : 0;
+    sum += tot[q];
+  }
+  int32_t run = block_excl_scan(sum, wsum);
+#pragma unroll
+  for (int q = 0; q < 1; ++q) {
+    if (lo + q < hi) s_off[lo + q] = run;
+    run += tot[q];
+  }
+  if (tid == 0) s_off[E + 1] = (int32_t)R;
+  __syncthreads();
+  for (int e = tid; e <= E; e += kRouteSmallThreads) {
+    offsets[e] = s_off[e];
+    if (e < E) counts[e] = s_off[e + 1] - s_off[e];
+  }
+  if (bm > 0) build_tile_table(s_off, E, bm, wsum, tile_expert, tile_mstart, meta);
+  __syncthreads();
+  // Stable scatter, kRouteSmallThreads rows at a time (as route_scatter_kernel):
+  // s_off[e] becomes the next free position of bucket e.
+  const int nbits = 32 - __clz(E);
+  const uint64_t lt_mask = (1ull << lane) - 1ull;
+  for (int64_t sub = 0; sub < R; sub += kRouteSmallThreads) {
+    for (int i = tid; i < NW * (E + 1); i += kRouteSmallThreads) wcnt[i] = 0;
+    __syncthreads();
+    const int64_t r = sub + tid;
+    const bool valid = r < R;
+    const int e = valid ? bucket_of(ids, r, R_ids, E_ids, E) : 0;
+    uint64_t match = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const uint64_t bal = __ballot((e >> b) & 1);
+      match &= ((e >> b) & 1) ? bal : ~bal;
+    }
+    const int rank = __popcll(match & lt_mask);
+    if (valid && rank == 0) wcnt[wave * (E + 1) + e] = __popcll(match);
+    __syncthreads();
+    if (valid) {
+      int32_t prev = 0;
+      for (int w = 0; w < wave; ++w) prev += wcnt[w * (E + 1) + e];
+      sorted_rows[s_off[e] + prev + rank] = (int32_t)r;
+    }
+    __syncthreads();
+    for (int b = tid; b <= E; b += kRouteSmallThreads) {
+      int32_t t = 0;
+      for (int w = 0; w < NW; ++w) t += wcnt[w * (E + 1) + b];
+      s_off[b] += t;
     }
     __syncthreads();
   }
@@ -438,6 +518,11 @@ template <typename IdxT>
 static int launch_route(const IdxT* ids, int64_t R, int64_t R_ids, int E_ids, int E, int32_t* blockcnt,
                         int32_t* counts, int32_t* offsets, int32_t* sorted_rows, int bm, int32_t* tile_expert,
                         int32_t* tile_mstart, int32_t* meta, hipStream_t st) {
+  if (R <= kRouteSmallRows && E <= kRouteSmallE) {
+    route_small_kernel<IdxT><<<1, kRouteSmallThreads, 0, st>>>(ids, R, R_ids, E_ids, E, counts, offsets, sorted_rows, bm,
+                                                          tile_expert, tile_mstart, meta);
+    return check_launch("route_small_kernel");
+  }
   const RoutePlan p = route_plan(R);
   const size_t hist_lds = (size_t)(E + 1) * sizeof(int32_t);
   route_count_kernel<IdxT><<<p.nb, kRouteThreads, hist_lds, st>>>(ids, R, R_ids, E_ids, E, p.chunk, p.nb, blockcnt);

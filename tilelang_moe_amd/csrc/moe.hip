@@ -183,10 +183,21 @@ extern "C" int moe_fused_moe(const void* x, const void* router_w, const void* sh
   int rc;
   // 1. Router (the reference takes router_weight as [E, Dh]: already the
   //    transposed layout the router GEMM reads).
-  if ((rc = moe_router_gemm(x, router_w, dtype, T, Dh, E, logits, ws, sub, stream))) return rc;
-  if ((rc = moe_topk_softmax_ex(logits, MOE_F32, T, E, E, k, w, idx, MOE_I32, MOE_TOPK_AUTO, MOE_SCORES_ALL, ws,
-                                sub, stream)))
-    return rc;
+  //    A split-H router GEMM leaves G partial rows per token: the selection
+  //    kernel sums them and selects (Convention A) in one launch.
+  if (E <= 256) {
+    const float* part = nullptr;
+    int G = 1;
+    if ((rc = router_gemm_logits_or_partials(x, router_w, dtype, T, Dh, E, logits, &part, &G, ws, sub, st))) return rc;
+    rc = G > 1 ? topk_select_partials(part, G, T, (int)E, (int)k, MOE_SCORES_ALL, w, idx, MOE_I32, st)
+               : moe_topk_softmax_ex(logits, MOE_F32, T, E, E, k, w, idx, MOE_I32, MOE_TOPK_AUTO, MOE_SCORES_ALL, ws,
+                                     sub, stream);
+  } else {
+    if ((rc = moe_router_gemm(x, router_w, dtype, T, Dh, E, logits, ws, sub, stream))) return rc;
+    rc = moe_topk_softmax_ex(logits, MOE_F32, T, E, E, k, w, idx, MOE_I32, MOE_TOPK_AUTO, MOE_SCORES_ALL, ws, sub,
+                             stream);
+  }
+  if (rc) return rc;
   if (moe_merged_shared(De, Ds)) {
     // 2. Routed experts and the shared one (expert E, rows T k .. T k + T - 1
     //    = tokens 0 .. T - 1): gate/up with the SwiGLU epilogue, then down

@@ -86,13 +86,15 @@ __global__ __launch_bounds__(256) void topk_bitonic_kernel(const T* __restrict__
 //    The K winners are staged in LDS for the softmax epilogue.
 // ===========================================================================
 // With PSUM (fp32 rows only) the row is the sum, in order g = 0..G-1, of the
-// G partial rows logits + g * gstride (split-H router GEMM partials).
+// G partial rows logits + g * gstride (split-H router GEMM partials), and
+// all_scores selects Convention A: exp(v - max) / sum over the whole row
+// (NaN everywhere if the row holds a NaN, as torch.softmax).
 template <typename T, int EPL, typename IdxT, bool PSUM = false>
 __global__ __launch_bounds__(256) void topk_select_kernel(const T* __restrict__ logits,
                                                           int64_t M, int N, int64_t ld,
                                                           int K, float* __restrict__ scores,
                                                           IdxT* __restrict__ indices, int G = 1,
-                                                          int64_t gstride = 0) {
+                                                          int64_t gstride = 0, bool all_scores = false) {
   extern __shared__ uint64_t win_all[];  // [waves][K]
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -130,6 +132,35 @@ __global__ __launch_bounds__(256) void topk_select_kernel(const T* __restrict__ 
     for (int i = 0; i < EPL; ++i) {
       const int idx = lane + kWave * i;
       c[i] = (live && idx < N) ? make_comp(key_of_bits(__float_as_uint(v[i])), idx) : 0;
+    }
+    if (all_scores) {
+      // Convention A: the normaliser over all N values, taken against the
+      // row maximum (the first winner; a NaN maximum makes every score NaN).
+      uint64_t best = c[0];
+#pragma unroll
+      for (int i = 1; i < EPL; ++i) best = umax64(best, c[i]);
+      const float m = value_of_key(comp_key(wave_max_u64(best)));
+      float sa = 0.0f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (lane + kWave * i < N) sa += expf(v[i] - m);
+      sa = wave_sum_f32(sa);
+      for (int r = 0; r < K; ++r) {
+        uint64_t b = c[0];
+#pragma unroll
+        for (int i = 1; i < EPL; ++i) b = umax64(b, c[i]);
+        b = wave_max_u64(b);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) c[i] = (c[i] == b) ? 0 : c[i];
+        if (lane == 0) win[r] = b;
+      }
+      __syncthreads();
+      if (!live) return;
+      for (int r = lane; r < K; r += kWave) {
+        const uint64_t w = win[r];
+        store_out(scores, indices, row * K + r, expf(value_of_key(comp_key(w)) - m) / sa, comp_idx(w));
+      }
+      return;
     }
   } else {
 #pragma unroll
@@ -1082,32 +1113,34 @@ static void launch_select_e(const T* x, int64_t M, int N, int64_t ld, int K, flo
 }
 
 template <typename IdxT, int EPL>
-static void launch_select_psum_e(const float* part, int G, int64_t M, int N, int K, float* s, IdxT* id,
+static void launch_select_psum_e(const float* part, int G, int64_t M, int N, int K, bool all, float* s, IdxT* id,
                                  hipStream_t st) {
   const int waves = 4;
   const int64_t grid = (M + waves - 1) / waves;
   const size_t lds = (size_t)waves * K * sizeof(uint64_t);
   topk_select_kernel<float, EPL, IdxT, true><<<dim3((unsigned)grid), dim3(waves * kWave), lds, st>>>(
-      part, M, N, N, K, s, id, G, M * N);
+      part, M, N, N, K, s, id, G, M * N, all);
 }
 
 template <typename IdxT>
-static int launch_select_psum(const float* part, int G, int64_t M, int N, int K, float* s, IdxT* id,
+static int launch_select_psum(const float* part, int G, int64_t M, int N, int K, bool all, float* s, IdxT* id,
                               hipStream_t st) {
   const int epl = (N + kWave - 1) / kWave;
-  if (epl <= 1) launch_select_psum_e<IdxT, 1>(part, G, M, N, K, s, id, st);
-  else if (epl <= 2) launch_select_psum_e<IdxT, 2>(part, G, M, N, K, s, id, st);
-  else if (epl <= 4) launch_select_psum_e<IdxT, 4>(part, G, M, N, K, s, id, st);
+  if (epl <= 1) launch_select_psum_e<IdxT, 1>(part, G, M, N, K, all, s, id, st);
+  else if (epl <= 2) launch_select_psum_e<IdxT, 2>(part, G, M, N, K, all, s, id, st);
+  else if (epl <= 4) launch_select_psum_e<IdxT, 4>(part, G, M, N, K, all, s, id, st);
   else return fail(MOE_EUNSUP, "partial-sum selection supports N <= 256");
   return check_launch("topk_select_kernel");
 }
 
-int topk_select_partials(const float* part, int G, int64_t M, int N, int K, float* scores, void* indices,
-                         int idx_dtype, hipStream_t st) {
+int topk_select_partials(const float* part, int G, int64_t M, int N, int K, int score_mode, float* scores,
+                         void* indices, int idx_dtype, hipStream_t st) {
   if (M == 0) return MOE_OK;
   if (K > N || G < 1) return fail(MOE_EINVAL, "topk_select_partials: need K <= N and G >= 1");
-  if (idx_dtype == MOE_I64) return launch_select_psum(part, G, M, N, K, scores, static_cast<int64_t*>(indices), st);
-  return launch_select_psum(part, G, M, N, K, scores, static_cast<int32_t*>(indices), st);
+  const bool all = score_mode == MOE_SCORES_ALL;
+  if (idx_dtype == MOE_I64)
+    return launch_select_psum(part, G, M, N, K, all, scores, static_cast<int64_t*>(indices), st);
+  return launch_select_psum(part, G, M, N, K, all, scores, static_cast<int32_t*>(indices), st);
 }
 
 template <typename T, typename IdxT>

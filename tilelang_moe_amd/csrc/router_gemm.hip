@@ -415,6 +415,20 @@ extern "C" size_t moe_router_workspace_size(int64_t T, int64_t H, int64_t E) {
   return router_ws_bytes(router_plan(T, H, E), T, E);
 }
 
+namespace moe {
+int router_gemm_logits_or_partials(const void* X, const void* Wt, int dtype, int64_t T, int64_t H, int64_t E,
+                                   float* logits, const float** part, int* G, void* workspace, size_t ws_bytes,
+                                   hipStream_t st) {
+  const RouterPlan p = router_plan(std::max<int64_t>(T, 1), std::max<int64_t>(H, 1), std::max<int64_t>(E, 1));
+  if (int rc = router_check("router_gemm", X, Wt, dtype, T, H, E, workspace, ws_bytes, p)) return rc;
+  *G = p.G;
+  *part = p.G > 1 ? reinterpret_cast<const float*>(static_cast<char*>(workspace) + kWsCtlBytes) : nullptr;
+  if (T == 0) return MOE_OK;
+  if (p.G == 1 && !logits) return fail(MOE_EINVAL, "router_gemm: null pointer");
+  return dispatch_router<0, int32_t>(dtype, p, X, Wt, T, H, E, 0, logits, nullptr, nullptr, workspace, st);
+}
+}  // namespace moe
+
 extern "C" int moe_router_gemm(const void* X, const void* Wt, int dtype, int64_t T, int64_t H, int64_t E,
                                float* logits, void* workspace, size_t ws_bytes, void* stream) {
   const RouterPlan p = router_plan(std::max<int64_t>(T, 1), std::max<int64_t>(H, 1), std::max<int64_t>(E, 1));
@@ -456,7 +470,7 @@ extern "C" int moe_router_topk_softmax(const void* X, const void* Wt, int dtype,
     if (int rc = dispatch_router<0, int32_t>(dtype, p, X, Wt, T, H, E, 0, nullptr, nullptr, nullptr, workspace, st))
       return rc;
     const float* part = reinterpret_cast<const float*>(static_cast<char*>(workspace) + kWsCtlBytes);
-    return topk_select_partials(part, p.G, T, (int)E, (int)K, scores, indices, idx_dtype, st);
+    return topk_select_partials(part, p.G, T, (int)E, (int)K, MOE_SCORES_TOPK, scores, indices, idx_dtype, st);
   }
   if (idx_dtype == MOE_I64)
     return dispatch_router<1, int64_t>(dtype, p, X, Wt, T, H, E, K, nullptr, scores, static_cast<int64_t*>(indices),
