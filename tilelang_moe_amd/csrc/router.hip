@@ -409,6 +409,9 @@ template <> struct VecLoad<Half16, 8> {
 // more than kBucketFixMax candidates switches to an LDS bitonic sort.
 // ---------------------------------------------------------------------------
 constexpr int kCandCap = 8192;
+constexpr int kOrdPad = 4;  // slack entries after tmp[] for the rank loop's unconditional loads
+// Dynamic LDS of the register-row kernels: cand[kCandCap], tmp[kCandCap + kOrdPad].
+constexpr size_t kRadixDynLds = (2 * kCandCap + kOrdPad) * sizeof(uint64_t);
 constexpr int kOrdBuckets = 2048;
 constexpr int kSample = kRadixThreads;
 
@@ -488,7 +491,7 @@ __device__ inline void order_prepare(uint32_t* hist, uint32_t* s_flag) {
 // keeps them, their buckets and their ranks in registers from the first
 // step to the last, so every step issues its U LDS accesses together.
 // hist[] and *s_flag must be zero (order_prepare) and published by a
-// barrier; tmp needs kCandCap entries, hist and bstart kOrdBuckets + 1.
+// barrier; tmp needs kCandCap + kOrdPad entries, hist and bstart kOrdBuckets + 1.
 template <int U, typename IdxT>
 __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t* cand, int C, uint32_t base, uint32_t rmax, int K,
                                          int64_t row, uint64_t* tmp, uint32_t* hist, uint32_t* bstart,
@@ -574,17 +577,20 @@ __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t
     rk[u] = beg[u];
     lmax = max(lmax, len[u]);
   }
-  // Four in-bucket loads per candidate are in flight before any compare.
+  // Four in-bucket loads per candidate are in flight before any compare;
+  // they are unconditional (tmp has kOrdPad entries of slack past kCandCap)
+  // so that adjacent pairs issue as one ds_read2_b64, and the compare masks
+  // the entries past the bucket.
   for (int j = 0; j < lmax; j += 4) {
     uint64_t t[U][4];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) t[u][q] = j + q < len[u] ? tmp[beg[u] + j + q] : 0ull;
+      for (int q = 0; q < 4; ++q) t[u][q] = tmp[beg[u] + j + q];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) rk[u] += t[u][q] > v[u];
+      for (int q = 0; q < 4; ++q) rk[u] += (j + q < len[u]) & (t[u][q] > v[u]);
   }
   MOE_PHASE(12);
   // The normaliser is summed exactly, in fixed point, so the scores are
@@ -707,7 +713,9 @@ __device__ inline uint32_t slot_col(int c0, int i) {
 
 template <int KPT>
 __device__ inline void rekey_if_special(uint32_t* key, bool special) {
-  if (__syncthreads_or(special)) {
+  // key_fast equals key_of_bits except for NaN and -0.0, so a thread that
+  // holds neither keeps its keys: no block-wide decision is needed.
+  if (special) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) key[i] = key[i] ? key_of_bits(bits_of_fast_key(key[i])) : 0u;  // 0 = padding
   }
@@ -800,7 +808,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   constexpr int NV = KPT / VEC;
   extern __shared__ uint64_t dyn[];
   uint64_t* cand = dyn;              // [kCandCap] in extraction order
-  uint64_t* tmp = dyn + kCandCap;    // [kCandCap] grouped by bucket
+  uint64_t* tmp = dyn + kCandCap;    // [kCandCap + kOrdPad] grouped by bucket
   __shared__ uint32_t hist[kRadixBins + 1];
   __shared__ uint32_t bstart[kOrdBuckets + 1];
   __shared__ uint32_t wsum[kRadixThreads / kWave];
@@ -825,7 +833,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   MOE_PHASE(1);
   bool special = false;
   keys_from_bits<T, VEC, KPT>(x, 0, N, key, special);
-  rekey_if_special<KPT>(key, special);  // has a barrier
+  rekey_if_special<KPT>(key, special);
   uint32_t kmax = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) kmax = max(kmax, key[i]);
@@ -950,7 +958,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   static_assert(KPT <= 32, "candidate bitmask is 32 bits");
   extern __shared__ uint64_t dyn[];
   uint64_t* cand = dyn;              // [kCandCap]
-  uint64_t* tmp = dyn + kCandCap;    // [kCandCap]
+  uint64_t* tmp = dyn + kCandCap;    // [kCandCap + kOrdPad]
   __shared__ uint32_t hist[kRadixBins + 1];
   __shared__ uint32_t bstart[kOrdBuckets + 1];
   __shared__ uint32_t wsum[kRadixThreads / kWave];
@@ -980,7 +988,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   MOE_PHASE(1);
   bool special = false;
   keys_from_bits<T, VEC, KPT>(x, c0, end, key, special);
-  rekey_if_special<KPT>(key, special);  // has a barrier
+  rekey_if_special<KPT>(key, special);
   uint32_t kmax = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) kmax = max(kmax, key[i]);
@@ -1220,11 +1228,11 @@ static int launch_radix_reg(const T* x, int64_t M, int N, int64_t ld, int K, flo
   if (!attr_set) {
     MOE_HIP_CHECK(hipFuncSetAttribute((const void*)topk_radix_reg_kernel<T, IdxT, VEC, KPT>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)(2 * kCandCap * sizeof(uint64_t))));
+                                      (int)(kRadixDynLds)));
     attr_set = true;
   }
   topk_radix_reg_kernel<T, IdxT, VEC, KPT><<<dim3((unsigned)M), dim3(kRadixThreads),
-                                              2 * kCandCap * sizeof(uint64_t), st>>>(x, M, N, ld, K, Kpad,
+                                              kRadixDynLds, st>>>(x, M, N, ld, K, Kpad,
                                                                                      s, id);
   return check_launch("topk_radix_reg_kernel");
 }
@@ -1296,14 +1304,14 @@ static int launch_radix_split(const T* x, int64_t M, int N, int64_t ld, int K, i
   if (!attr_set) {
     MOE_HIP_CHECK(hipFuncSetAttribute((const void*)topk_radix_split_kernel<T, IdxT, VEC, KPT>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)(2 * kCandCap * sizeof(uint64_t))));
+                                      (int)(kRadixDynLds)));
     attr_set = true;
   }
   SplitRowCtl* ctl = static_cast<SplitRowCtl*>(ws);
   uint64_t* gcand = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + kWsCtlBytes);
   const int64_t grid = (M + 7) / 8 * 8 * G;
   topk_radix_split_kernel<T, IdxT, VEC, KPT><<<dim3((unsigned)grid), dim3(kRadixThreads),
-                                                2 * kCandCap * sizeof(uint64_t), st>>>(
+                                                kRadixDynLds, st>>>(
       x, M, N, ld, K, next_pow2(K), G, slice, s, id, ctl, gcand);
   return check_launch("topk_radix_split_kernel");
 }
