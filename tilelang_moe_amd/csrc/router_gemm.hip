@@ -55,78 +55,6 @@ __global__ __launch_bounds__(256) void router_transpose_kernel(const uint16_t* _
   }
 }
 
-// ---------------------------------------------------------------------------
-// Segment helpers: a segment is one 16-lane DPP row of the wave.
-// ---------------------------------------------------------------------------
-__device__ inline uint32_t seg16_shfl(uint32_t v, int src) {
-  return (uint32_t)__builtin_amdgcn_ds_bpermute(((int)(__lane_id() & ~15u) + src) << 2, (int)v);
-}
-__device__ inline uint64_t seg16_shfl_u64(uint64_t v, int src) {
-  return ((uint64_t)seg16_shfl((uint32_t)(v >> 32), src) << 32) | seg16_shfl((uint32_t)v, src);
-}
-__device__ inline uint32_t seg16_incl_scan(uint32_t x) {
-  x += dpp<kDppRowShr1>(0u, x);
-  x += dpp<kDppRowShr2>(0u, x);
-  x += dpp<kDppRowShr4>(0u, x);
-  x += dpp<kDppRowShr8>(0u, x);
-  return x;
-}
-__device__ inline uint32_t seg16_sum(uint32_t x) {
-  x += xor_lanes<1>(x);
-  x += xor_lanes<2>(x);
-  x += xor_lanes<4>(x);
-  x += xor_lanes<8>(x);
-  return x;
-}
-// Descending bitonic sort of one value per lane over the segment.
-template <typename V>
-__device__ inline V seg16_sort_desc(V v) {
-  const int pos = __lane_id() & 15;
-#pragma unroll
-  for (int k2 = 2; k2 <= 16; k2 <<= 1) {
-#pragma unroll
-    for (int j = k2 >> 1; j > 0; j >>= 1) {
-      V o;
-      if constexpr (sizeof(V) == 8) o = xor_lanes_u64(v, j);
-      else o = (V)__float_as_uint(xor_lanes_f32(__uint_as_float((uint32_t)v), j));
-      const bool desc = (pos & k2) == 0, lower = (pos & j) == 0;
-      v = (desc == lower) ? (v > o ? v : o) : (v < o ? v : o);
-    }
-  }
-  return v;
-}
-
-// Top-K (K <= 16) of one row held by a segment: lane pos holds the keys of
-// columns pos + 16 i (key 0 = no element).  The K-th largest of the 16
-// lane maxima, tau, is a lower bound of the row's K-th largest key (K
-// lanes hold a key >= tau), so every winner is among the keys >= tau.
-// Those are compacted into the segment's 16 LDS slots and sorted as
-// composites (key desc, column asc); lane r < K returns winner r in `out`.
-// Returns false, leaving `out` alone, when K > 16 or more than 16 keys are
-// >= tau (segment-uniform).
-template <int EPL>
-__device__ inline bool seg16_topk_filtered(const uint32_t (&key)[EPL], int K, uint64_t* scratch, uint64_t& out) {
-  if (K > 16) return false;
-  const int pos = __lane_id() & 15;
-  uint32_t m = key[0];
-#pragma unroll
-  for (int i = 1; i < EPL; ++i) m = max(m, key[i]);
-  const uint32_t tau = max(seg16_shfl(seg16_sort_desc(m), K - 1), 1u);
-  uint32_t cnt = 0;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) cnt += key[i] >= tau;
-  const uint32_t total = seg16_sum(cnt);
-  if (total > 16) return false;
-  uint32_t p = seg16_incl_scan(cnt) - cnt;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i)
-    if (key[i] >= tau) scratch[p++] = make_comp(key[i], (uint32_t)(pos + 16 * i));
-  __builtin_amdgcn_wave_barrier();  // LDS ops of one wave complete in order
-  const uint64_t c = seg16_sort_desc<uint64_t>(pos < (int)total ? scratch[pos] : 0);
-  __builtin_amdgcn_wave_barrier();  // the slots are reused by the next row
-  out = pos < K ? c : 0;
-  return true;
-}
 
 using CfgRouter128 = GemmCfg<64, 128, 2, 2, 64, 3>;     // 4 waves of 32x64, 72 KB LDS
 using CfgRouter256 = GemmCfg<64, 256, 1, 4, 64, 2>;     // 4 waves of 64x64, 80 KB LDS
@@ -235,7 +163,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void router_gemm_kernel(
       }
       // Lane pos ends with winners pos and pos + 16 (composites, 0 = none).
       uint64_t win[kRouterMaxK / kRouterSeg] = {0, 0};
-      if (!seg16_topk_filtered<EPL>(key, K, seg_scratch, win[0])) {
+      if (!seg16_topk_filtered<EPL>(key, K, seg_scratch, win[0], [](int p, int i) { return p + kRouterSeg * i; })) {
         // Rounds of a segment max: K > 16, or more than 16 keys at or
         // above the filter (heavy ties).
         uint64_t c[EPL];
