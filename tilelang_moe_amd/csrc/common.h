@@ -288,6 +288,24 @@ __device__ inline uint64_t wave_max_u64(uint64_t x) {
   return umax64(umax64(a, b), umax64(c, d));
 }
 
+__device__ inline uint32_t xor_lanes_u32(uint32_t x, int m) {
+  return __float_as_uint(xor_lanes_f32(__uint_as_float(x), m));
+}
+
+// 32-bit composites of bfloat16 values: the order-preserving key of a
+// bfloat16 value is 16 bits wide (the key of its fp32 widening shifted
+// right by 16: the dropped bits are constant for a given sign), so key and
+// column (< 65536) pack into one unique 32-bit composite
+// (key16 << 16) | (0xFFFF - column): larger means a larger value, then a
+// lower column; 0 is below every real composite.
+__device__ inline uint32_t comp16_of(uint32_t bits16, int col) {
+  return ((key_of_bits(bits16 << 16) >> 16) << 16) | (0xFFFFu - (uint32_t)col);
+}
+__device__ inline float value_of_comp16(uint32_t c) {
+  const uint32_t k16 = c >> 16;
+  return value_of_key((k16 << 16) | ((k16 & 0x8000u) ? 0u : 0xFFFFu));
+}
+
 // ---------------------------------------------------------------------------
 // Segment helpers: a segment is one 16-lane DPP row of the wave.
 // ---------------------------------------------------------------------------

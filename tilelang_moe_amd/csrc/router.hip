@@ -14,6 +14,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace moe {
 
@@ -34,6 +35,7 @@ __device__ inline void store_out(float* scores, IdxT* indices, int64_t off, floa
 //    Here a segment of S lanes (S = next pow2 >= N) holds one row, so a wave
 //    sorts 64/S rows at once and every compare-exchange is a lane shuffle.
 // ===========================================================================
+//    bfloat16 rows sort 32-bit composites (comp16_of) instead of 64-bit ones.
 template <typename T, int S, typename IdxT>
 __global__ __launch_bounds__(256) void topk_bitonic_kernel(const T* __restrict__ logits,
                                                            int64_t M, int N, int64_t ld,
@@ -44,6 +46,30 @@ __global__ __launch_bounds__(256) void topk_bitonic_kernel(const T* __restrict__
   const int wave = threadIdx.x / kWave;
   const int pos = lane & (S - 1);
   const int64_t row = ((int64_t)blockIdx.x * (blockDim.x / kWave) + wave) * RPW + lane / S;
+
+  if constexpr (std::is_same<T, uint16_t>::value) {
+    uint32_t c = (row < M && pos < N) ? comp16_of(logits[row * ld + pos], pos) : 0u;
+#pragma unroll
+    for (int k = 2; k <= S; k <<= 1) {
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const uint32_t o = xor_lanes_u32(c, j);
+        const bool desc = (pos & k) == 0;
+        const bool lower = (pos & j) == 0;
+        c = (desc == lower) ? max(c, o) : min(c, o);
+      }
+    }
+    uint32_t cmax = c;  // the segment head holds the largest
+#pragma unroll
+    for (int j = 1; j < S; j <<= 1) cmax = max(cmax, xor_lanes_u32(cmax, j));
+    const float vmax = value_of_comp16(cmax);
+    const float e = pos < K ? expf(value_of_comp16(c) - vmax) : 0.0f;
+    float sum = e;
+#pragma unroll
+    for (int j = 1; j < S; j <<= 1) sum += xor_lanes_f32(sum, j);
+    if (row < M && pos < K) store_out(scores, indices, row * K + pos, e / sum, 0xFFFFu - (c & 0xFFFFu));
+    return;
+  }
 
   uint64_t c = 0;  // padding composite sorts last
   if (row < M && pos < N) c = make_comp(key_of_bits(Elem<T>::bits(logits + row * ld + pos)), pos);
@@ -190,6 +216,55 @@ __global__ __launch_bounds__(256) void topk_select_kernel(const T* __restrict__ 
     const uint64_t w = win[r];
     store_out(scores, indices, row * K + r, expf(value_of_key(comp_key(w)) - vmax) / sum,
               comp_idx(w));
+  }
+}
+
+// ===========================================================================
+// 2c. Selection for bfloat16 rows: the order-preserving key of a bfloat16
+//     value is 16 bits wide (the key of its fp32 widening shifted right by
+//     16: the dropped bits are constant for a given sign), so the key and
+//     the column (N <= 65536) pack into one unique 32-bit composite
+//     (key16 << 16) | (0xFFFF - column): a larger composite is a larger
+//     value, then a lower column, as everywhere.  A round of the selection is
+//     then a 32-bit wave max (DPP max steps) instead of 64-bit
+//     compare-and-select butterflies.  Same results as topk_select_kernel.
+// ===========================================================================
+
+template <int EPL, typename IdxT>
+__global__ __launch_bounds__(256) void topk_select16_kernel(const uint16_t* __restrict__ logits, int64_t M, int N,
+                                                            int64_t ld, int K, float* __restrict__ scores,
+                                                            IdxT* __restrict__ indices) {
+  extern __shared__ uint32_t win16_all[];  // [waves][K]
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + wave;
+  const bool live = row < M;  // wave-uniform
+  uint32_t* win = win16_all + (size_t)wave * K;
+  const uint16_t* x = logits + (live ? row : 0) * ld;
+  uint32_t c[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int idx = lane + kWave * i;
+    c[i] = (live && idx < N) ? comp16_of(x[idx], idx) : 0u;  // 0: below every real composite
+  }
+  for (int r = 0; r < K; ++r) {
+    uint32_t best = c[0];
+#pragma unroll
+    for (int i = 1; i < EPL; ++i) best = max(best, c[i]);
+    best = wave_max_u32(best);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) c[i] = c[i] == best ? 0u : c[i];
+    if (lane == 0) win[r] = best;
+  }
+  __syncthreads();
+  if (!live) return;
+  const float vmax = value_of_comp16(win[0]);
+  float sum = 0.0f;
+  for (int r = lane; r < K; r += kWave) sum += expf(value_of_comp16(win[r]) - vmax);
+  sum = wave_sum_f32(sum);
+  for (int r = lane; r < K; r += kWave) {
+    const uint32_t w = win[r];
+    store_out(scores, indices, row * K + r, expf(value_of_comp16(w) - vmax) / sum, 0xFFFFu - (w & 0xFFFFu));
   }
 }
 
@@ -1234,6 +1309,15 @@ static int launch_seg_e(const T* x, int64_t M, int N, int64_t ld, int K, float* 
   return check_launch("topk_seg_kernel");
 }
 
+template <typename IdxT, int EPL>
+static void launch_select16_e(const uint16_t* x, int64_t M, int N, int64_t ld, int K, float* s, IdxT* id,
+                              hipStream_t st) {
+  const int waves = 4;
+  const int64_t grid = (M + waves - 1) / waves;
+  topk_select16_kernel<EPL, IdxT><<<dim3((unsigned)grid), dim3(waves * kWave), (size_t)waves * K * 4, st>>>(
+      x, M, N, ld, K, s, id);
+}
+
 template <typename T, typename IdxT>
 static int launch_select(const T* x, int64_t M, int N, int64_t ld, int K, float* s, IdxT* id,
                          hipStream_t st) {
@@ -1243,6 +1327,16 @@ static int launch_select(const T* x, int64_t M, int N, int64_t ld, int K, float*
   if (K <= 16 && N <= 128 && M <= (int64_t)INT32_MAX) {
     if (N <= 64) return launch_seg_e<T, IdxT, 4>(x, M, N, ld, K, s, id, st);
     return launch_seg_e<T, IdxT, 8>(x, M, N, ld, K, s, id, st);
+  }
+  if constexpr (std::is_same<T, uint16_t>::value) {  // bfloat16: 32-bit composites
+    const int epl = (N + kWave - 1) / kWave;
+    if (epl <= 1) launch_select16_e<IdxT, 1>(x, M, N, ld, K, s, id, st);
+    else if (epl <= 2) launch_select16_e<IdxT, 2>(x, M, N, ld, K, s, id, st);
+    else if (epl <= 4) launch_select16_e<IdxT, 4>(x, M, N, ld, K, s, id, st);
+    else if (epl <= 8) launch_select16_e<IdxT, 8>(x, M, N, ld, K, s, id, st);
+    else if (epl <= 16) launch_select16_e<IdxT, 16>(x, M, N, ld, K, s, id, st);
+    else return fail(MOE_EUNSUP, "selection router supports N <= 1024");
+    return check_launch("topk_select16_kernel");
   }
   const int epl = (N + kWave - 1) / kWave;
   if (epl <= 1) launch_select_e<T, IdxT, 1>(x, M, N, ld, K, s, id, st);
