@@ -57,6 +57,7 @@ __global__ __launch_bounds__(256) void router_transpose_kernel(const uint16_t* _
 
 
 using CfgRouter128 = GemmCfg<64, 128, 2, 2, 64, 3>;     // 4 waves of 32x64, 72 KB LDS
+using CfgRouter192 = GemmCfg<64, 192, 2, 2, 64, 2>;     // 4 waves of 32x96, 64 KB LDS: two per CU
 using CfgRouter256 = GemmCfg<64, 256, 1, 4, 64, 2>;     // 4 waves of 64x64, 80 KB LDS
 constexpr int kRouterSeg = 16;                         // lanes per row in the fused epilogue
 constexpr int kRouterMaxK = 2 * kRouterSeg;            // winners held two per lane
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(256) void router_reduce_kernel(const float* __restr
 // Host side.
 // ---------------------------------------------------------------------------
 struct RouterPlan {
-  int cfg;  // 0: 64x128 tiles, 1: 64x256 tiles
+  int cfg;  // 0: 64x128 tiles, 1: 64x256 tiles, 2: 64x192 tiles
   int NT, G;
   int64_t tiles, kchunk;
   size_t part_floats;
@@ -263,8 +264,11 @@ static RouterPlan router_plan_cfg(int cfg, int64_t T, int64_t H, int64_t E) {
 }
 
 static RouterPlan router_plan(int64_t T, int64_t H, int64_t E) {
-  return E <= CfgRouter128::BN ? router_plan_cfg<CfgRouter128>(0, T, H, E)
-                               : router_plan_cfg<CfgRouter256>(1, T, H, E);
+  // The narrowest tile that holds all E experts: the padding columns still
+  // cost their weight-row copies.
+  return E <= CfgRouter128::BN   ? router_plan_cfg<CfgRouter128>(0, T, H, E)
+         : E <= CfgRouter192::BN ? router_plan_cfg<CfgRouter192>(2, T, H, E)
+                                 : router_plan_cfg<CfgRouter256>(1, T, H, E);
 }
 
 // Bytes of the split-H partial logits [G][T][E] (split plans only).
@@ -301,8 +305,11 @@ static int dispatch_router(int dtype, const RouterPlan& p, const void* X, const 
     using C = decltype(cfg_tag);
     return launch_router<TT, C, EPI, IdxT>(p, x, wt, T, H, (int)E, (int)K, logits, scores, idx, ws, st);
   };
-  if (dtype == MOE_BF16) return p.cfg == 0 ? run(uint16_t{}, CfgRouter128{}) : run(uint16_t{}, CfgRouter256{});
-  return p.cfg == 0 ? run(Half16{}, CfgRouter128{}) : run(Half16{}, CfgRouter256{});
+  if (dtype == MOE_BF16)
+    return p.cfg == 0 ? run(uint16_t{}, CfgRouter128{}) : p.cfg == 2 ? run(uint16_t{}, CfgRouter192{})
+                                                                      : run(uint16_t{}, CfgRouter256{});
+  return p.cfg == 0 ? run(Half16{}, CfgRouter128{}) : p.cfg == 2 ? run(Half16{}, CfgRouter192{})
+                                                                  : run(Half16{}, CfgRouter256{});
 }
 
 static int router_check(const char* fn, const void* X, const void* Wt, int dtype, int64_t T, int64_t H, int64_t E,
