@@ -101,17 +101,19 @@ def test_router_gemm_logits(cuda, T, H, E):
 
 @pytest.mark.parametrize("T,H,E,k", [(256, 3584, 64, 8), (256, 4096, 128, 8), (256, 5120, 160, 6),
                                      (1, 512, 160, 6), (63, 1032, 256, 32), (65, 776, 8, 1),
-                                     (3000, 2048, 160, 6), (4096, 1024, 128, 8), (513, 4096, 256, 8)])
+                                     (3000, 2048, 160, 6), (4096, 1024, 128, 8), (513, 4096, 256, 8),
+                                     (16384, 5120, 160, 6)])
 def test_fused_router_parity(cuda, T, H, E, k):
     X, W = make(T, H, E, seed=7 * T + E + k)
     check_fused(X, W, k)
 
 
-# H < 1024 is never split over workgroups, so these run the selection
-# epilogue inside the GEMM kernel: the filtered path (K <= 16) and the
-# rounds path (K > 16), E not a multiple of 16, and the benchmark shape.
-@pytest.mark.parametrize("T,H,E,k", [(3000, 512, 160, 6), (2000, 520, 256, 32), (1000, 776, 64, 16),
-                                     (777, 1016, 200, 17), (64, 8, 33, 3), (16384, 5120, 160, 6)])
+# H < 512 is never split over workgroups (splits keep >= 256 of H), nor is a
+# problem of >= 512 tiles, so these run the selection epilogue inside the
+# GEMM kernel: the filtered path (K <= 16) and the rounds path (K > 16), E
+# not a multiple of 16, all three tile widths (128, 192, 256 experts).
+@pytest.mark.parametrize("T,H,E,k", [(3000, 504, 160, 6), (2000, 264, 256, 32), (1000, 392, 64, 16),
+                                     (777, 456, 200, 17), (64, 8, 33, 3), (40000, 256, 160, 6)])
 def test_fused_router_epilogue_in_kernel(cuda, T, H, E, k):
     X, W = make(T, H, E, seed=T + H + k, scale=0.1)
     check_fused(X, W, k)
