@@ -116,6 +116,35 @@ def test_infinities_and_nan(cuda):
             check(x[:, :n].contiguous(), 4, algo, scores_nan_ok=True)
 
 
+@pytest.mark.parametrize("k", [1, 100, 2048, 6000, 8192])
+def test_radix_adversarial_rows_full_length(cuda, k):
+    """Rows of the C2 length whose value distributions drive the radix
+    kernel off its common path: candidates crowding one ordering bucket
+    (bitonic fallback), a narrow key range, ties at the K-th value (exact
+    threshold, lowest columns among the ties), more candidates than the
+    candidate buffer holds, two clusters, a heavy tail."""
+    n = 32768
+    g = torch.Generator(device="cpu").manual_seed(k)
+    rows = [
+        1e-4 * torch.arange(n, dtype=torch.float32),                 # sorted, unique (scores stay normal floats)
+        torch.flip(1e-4 * torch.arange(n, dtype=torch.float32), [0]),  # reverse sorted
+        1.0 + 1e-6 * torch.randn(n, generator=g),                    # narrow key range
+        torch.cat([torch.zeros(n // 2), 100.0 + torch.rand(n // 2, generator=g)]),  # two clusters
+        torch.empty(n).exponential_(1.0, generator=g),                # heavy tail
+        torch.randint(0, 3, (n,), generator=g).float(),               # three values: ties everywhere
+    ]
+    ties = torch.randn(n, generator=g)
+    kth = torch.sort(ties, descending=True).values[min(k, n) - 1]
+    ties[torch.randperm(n, generator=g)[:5000]] = kth                 # many copies of the K-th value
+    rows.append(ties)
+    crowd = torch.randn(n, generator=g)
+    crowd[:3000] = 3.0 + 1e-7 * torch.arange(3000, dtype=torch.float32)  # one dense bucket near the top
+    rows.append(crowd)
+    x = torch.stack(rows).to(cuda)
+    for _ in range(2):
+        check(x, k, "radix")
+
+
 @pytest.mark.parametrize("m,n,k", [(8, 40000, 100), (64, 65536, 2048), (3, 65536, 512), (17, 50000, 4096),
                                    (2, 300000, 16), (256, 32769, 64), (5, 1 << 20, 8)])
 def test_split_rows(cuda, m, n, k):
