@@ -463,8 +463,8 @@ template <> struct VecLoad<Half16, 8> {
 };
 
 // ===========================================================================
-// 2b. Segment selection, N <= 128 and K <= 16 (e.g. C1 of the
-//     benchmarks).  One 16-lane DPP row per
+// 2b. Segment selection, N <= 128 and K <= 16 (e.g. the DeepSeek-V2
+//     router shape, 128 experts, top-6).  One 16-lane DPP row per
 //     row of the input, so a wave (one workgroup) takes four rows.
 //     Lane pos holds columns pos*EPL .. pos*EPL + EPL - 1 (16-byte loads when
 //     the rows are full and aligned).  The K-th largest of the 16 lane maxima
@@ -1321,8 +1321,8 @@ static void launch_select16_e(const uint16_t* x, int64_t M, int N, int64_t ld, i
 template <typename T, typename IdxT>
 static int launch_select(const T* x, int64_t M, int N, int64_t ld, int K, float* s, IdxT* id,
                          hipStream_t st) {
-  // Rows of up to 128 with K <= 16 take the segment kernel (measured: C1
-  // fp32 [320,128] K=6 2.9 us against 3.9 us); at N = 256 (16 keys per lane)
+  // Rows of up to 128 with K <= 16 take the segment kernel (measured: fp32
+  // [320,128] K=6 2.9 us against 3.9 us); at N = 256 (16 keys per lane)
   // the one-wave-per-row kernel below is as fast or faster.
   if (K <= 16 && N <= 128 && M <= (int64_t)INT32_MAX) {
     if (N <= 64) return launch_seg_e<T, IdxT, 4>(x, M, N, ld, K, s, id, st);
