@@ -94,8 +94,10 @@ def test_python_api_rejects_cpu_tensors():
 def test_router_gemm_host_checks():
     L = _lib.lib()
     nul = None
-    # workspace: control block alone for large T, plus split partials for small T
-    assert L.moe_router_workspace_size(16384, 5120, 160) == 4096
+    # workspace: control block alone once there are 512 tiles (32768 tokens of
+    # 64-row tiles), plus the split-H partials [G][T][E] below that
+    assert L.moe_router_workspace_size(32768, 5120, 160) == 4096
+    assert L.moe_router_workspace_size(16384, 5120, 160) == 4096 + 2 * 16384 * 160 * 4
     assert L.moe_router_workspace_size(256, 5120, 160) > 4096
     # fused limits: E > 256 or K > 32 -> unsupported; K > E -> invalid
     assert L.moe_router_topk_softmax(16, 16, 1, 4, 64, 300, 8, 16, 16, 3, 16, 1 << 20, nul) == _lib.MOE_EUNSUP
