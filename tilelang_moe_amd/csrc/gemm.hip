@@ -66,10 +66,10 @@ __device__ inline int32_t block_excl_scan(int32_t v, int32_t* wsum) {
   const int nw = blockDim.x / kWave;
   const int32_t incl = (int32_t)wave_incl_scan((uint32_t)v);
   if (lane == kWave - 1) wsum[wave] = incl;
-  __syncthreads();
+  lds_barrier();
   int32_t base = 0;
   for (int w = 0; w < nw; ++w) base += (w < wave) ? wsum[w] : 0;
-  __syncthreads();
+  lds_barrier();
   return base + incl - v;
 }
 
@@ -212,11 +212,16 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
 }
 
 // The whole routing sort in one workgroup of kRouteSmallThreads, for small
-// problems (R <= kRouteSmallRows, E <= kRouteSmallE): the histogram, the
-// segment offsets, the tile table (bm > 0) and the stable scatter of
-// route_count / route_scan / route_scatter, without their two launches and
-// the blockcnt round trip.  The scatter takes kRouteSmallThreads rows per
-// round, so it is kept to a few rounds.
+// problems (R <= kRouteSmallRows, E <= kRouteSmallE): bucket counts, segment
+// offsets, the tile table (bm > 0) and the stable scatter of route_count /
+// route_scan / route_scatter, without their two launches and the blockcnt
+// round trip.  Thread tid owns rows tid + kRouteSmallThreads q (q < PER), so
+// row order is (q, wave, lane) order.  Each wave counts, per round q, the
+// rows of every bucket in one ballot pass; a wave scan turns each bucket's
+// column of (q, wave) counts into exclusive prefixes (their total is the
+// bucket count); every row then goes to
+//   segment start + rows of its bucket in earlier (q, wave) + rank in wave,
+// with no further barrier.
 constexpr int kRouteSmallThreads = 1024;
 constexpr int64_t kRouteSmallRows = 4096;
 constexpr int kRouteSmallE = 256;
@@ -227,68 +232,67 @@ __global__ __launch_bounds__(kRouteSmallThreads) void route_small_kernel(
     int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_rows, int bm, int32_t* __restrict__ tile_expert,
     int32_t* __restrict__ tile_mstart, int32_t* __restrict__ meta) {
   constexpr int NW = kRouteSmallThreads / kWave;
-  __shared__ int32_t s_off[kRouteSmallE + 2];     // counts, then segment starts
-  __shared__ int32_t wcnt[NW * (kRouteSmallE + 1)];
+  constexpr int PER = (int)(kRouteSmallRows / kRouteSmallThreads);
+  constexpr int NS = PER * NW;  // (round, wave) segments
+  static_assert(kRouteSmallRows % kRouteSmallThreads == 0, "whole rounds of rows");
+  static_assert(kRouteSmallRows <= 65535, "prefixes are 16-bit");
+  static_assert(kRouteSmallE + 1 <= kRouteSmallThreads, "one thread per bucket");
+  static_assert(NS == kWave, "a bucket's segment column is one wave");
+  __shared__ int32_t s_off[kRouteSmallE + 2];                 // segment starts
+  __shared__ uint16_t segcnt[NS * (kRouteSmallE + 1)];        // [segment][bucket]
   __shared__ int32_t wsum[NW];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  for (int e = tid; e <= E; e += kRouteSmallThreads) s_off[e] = 0;
-  __syncthreads();
-  for (int64_t r = tid; r < R; r += kRouteSmallThreads) atomicAdd(&s_off[bucket_of(ids, r, R_ids, E_ids, E)], 1);
-  __syncthreads();
-  // Exclusive scan of the E + 1 bucket counts (contiguous runs per thread).
-  const int per = (E + 1 + kRouteSmallThreads - 1) / kRouteSmallThreads;  // 1 for E <= 256
-  const int lo = std::min(E + 1, tid * per), hi = std::min(E + 1, lo + per);
-  int32_t tot[1], sum = 0;
+  const int W1 = E + 1;  // buckets: experts, then ids outside [0, E)
+  int bk[PER];
 #pragma unroll
-  for (int q = 0; q < 1; ++q) {
-    tot[q] = (lo + q < hi) ? s_off[lo + q] : 0;
-    sum += tot[q];
+  for (int q = 0; q < PER; ++q) {
+    const int64_t r = tid + (int64_t)kRouteSmallThreads * q;
+    bk[q] = r < R ? bucket_of(ids, r, R_ids, E_ids, E) : -1;
   }
-  int32_t run = block_excl_scan(sum, wsum);
-#pragma unroll
-  for (int q = 0; q < 1; ++q) {
-    if (lo + q < hi) s_off[lo + q] = run;
-    run += tot[q];
-  }
-  if (tid == 0) s_off[E + 1] = (int32_t)R;
-  __syncthreads();
-  for (int e = tid; e <= E; e += kRouteSmallThreads) {
-    offsets[e] = s_off[e];
-    if (e < E) counts[e] = s_off[e + 1] - s_off[e];
-  }
-  if (bm > 0) build_tile_table(s_off, E, bm, wsum, tile_expert, tile_mstart, meta);
-  __syncthreads();
-  // Stable scatter, kRouteSmallThreads rows at a time (as route_scatter_kernel):
-  // s_off[e] becomes the next free position of bucket e.
+  for (int i = tid; i < NS * W1; i += kRouteSmallThreads) segcnt[i] = 0;
+  lds_barrier();
+  // Lanes holding the same bucket: intersect the ballots of every bit.
   const int nbits = 32 - __clz(E);
   const uint64_t lt_mask = (1ull << lane) - 1ull;
-  for (int64_t sub = 0; sub < R; sub += kRouteSmallThreads) {
-    for (int i = tid; i < NW * (E + 1); i += kRouteSmallThreads) wcnt[i] = 0;
-    __syncthreads();
-    const int64_t r = sub + tid;
-    const bool valid = r < R;
-    const int e = valid ? bucket_of(ids, r, R_ids, E_ids, E) : 0;
+  int rank[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    rank[q] = 0;
+    if ((int64_t)kRouteSmallThreads * q >= R) continue;  // no rows in this round
+    const bool valid = bk[q] >= 0;
+    const int e = valid ? bk[q] : 0;
     uint64_t match = __ballot(valid);
     for (int b = 0; b < nbits; ++b) {
       const uint64_t bal = __ballot((e >> b) & 1);
       match &= ((e >> b) & 1) ? bal : ~bal;
     }
-    const int rank = __popcll(match & lt_mask);
-    if (valid && rank == 0) wcnt[wave * (E + 1) + e] = __popcll(match);
-    __syncthreads();
-    if (valid) {
-      int32_t prev = 0;
-      for (int w = 0; w < wave; ++w) prev += wcnt[w * (E + 1) + e];
-      sorted_rows[s_off[e] + prev + rank] = (int32_t)r;
-    }
-    __syncthreads();
-    for (int b = tid; b <= E; b += kRouteSmallThreads) {
-      int32_t t = 0;
-      for (int w = 0; w < NW; ++w) t += wcnt[w * (E + 1) + b];
-      s_off[b] += t;
-    }
-    __syncthreads();
+    rank[q] = __popcll(match & lt_mask);
+    if (valid && rank[q] == 0) segcnt[(q * NW + wave) * W1 + e] = (uint16_t)__popcll(match);
   }
+  lds_barrier();
+  // Wave w scans the columns of buckets w, w + NW, ...: lane = segment.
+  for (int e = wave; e < W1; e += NW) {
+    const uint32_t c = segcnt[lane * W1 + e];
+    const uint32_t incl = wave_incl_scan(c);
+    segcnt[lane * W1 + e] = (uint16_t)(incl - c);
+    if (lane == kWave - 1) s_off[e] = (int32_t)incl;  // the bucket's count
+  }
+  lds_barrier();
+  const int32_t tot = tid < W1 ? s_off[tid] : 0;
+  const int32_t start = block_excl_scan(tot, wsum);
+  if (tid < W1) {
+    s_off[tid] = start;
+    offsets[tid] = start;
+    if (tid < E) counts[tid] = tot;
+  }
+  if (tid == 0) s_off[W1] = (int32_t)R;
+  lds_barrier();
+  if (bm > 0) build_tile_table(s_off, E, bm, wsum, tile_expert, tile_mstart, meta);
+#pragma unroll
+  for (int q = 0; q < PER; ++q)
+    if (bk[q] >= 0)
+      sorted_rows[s_off[bk[q]] + segcnt[(q * NW + wave) * W1 + bk[q]] + rank[q]] =
+          (int32_t)(tid + kRouteSmallThreads * q);
 }
 
 // ---------------------------------------------------------------------------
@@ -298,7 +302,7 @@ constexpr int kMinBM = 64;  // smallest M tile of any configuration (workspace s
 
 using CfgHuge = GemmCfg<256, 256, 2, 4, 64, 2, 1>;   // 8 waves of 128x64, 128 KB LDS, 1 per CU
 using CfgLarge = GemmCfg<128, 256, 2, 2, 32, 2, 2>;  // 4 waves of 64x128,  48 KB LDS, 2 per CU
-using CfgSmall = GemmCfg<64, 128, 2, 2, 64, 3>;      // 4 waves of 32x64,   72 KB LDS
+using CfgSmall = GemmCfg<64, 128, 2, 2, 64, 3, 2>;   // 4 waves of 32x64,   72 KB LDS, 2 per CU
 
 // EPI 0: Y = X W^T.  EPI 1 (SwiGLU): Y = silu(X Wg^T) * (X Wu^T) with W = Wg and
 // W2 = Wu, both [E, I, H]; a tile then covers BN/2 output columns, its even
