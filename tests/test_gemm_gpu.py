@@ -50,10 +50,13 @@ def make(T, H, I, E, seed=0, dtype=torch.bfloat16, device="cuda"):
 # ---------------------------------------------------------------------------
 # Routing sort
 # ---------------------------------------------------------------------------
-# Up to 4096 rows and 256 experts one workgroup sorts (route_small_kernel);
-# (4096, 256) is its largest case, (4097, 256) and (2048, 257) just beyond.
-# The three-kernel sort takes the rest; (8192, 1) puts every row in one bucket.
-@pytest.mark.parametrize("R,E", [(0, 4), (1, 1), (255, 8), (256, 8), (257, 8), (1000, 1), (4096, 256), (4097, 256),
+# One workgroup sorts up to 2048 rows of up to 256 experts, and up to 4096
+# rows of 256 experts (route_small_kernel): (2048, 8), (2048, 256) and
+# (4096, 256) are its largest cases, (2049, 8), (4097, 256) and (2048, 257)
+# just beyond.  Above 255 experts the sort takes three kernels, below it two
+# (the scan folded into the scatter); (8192, 1) puts every row in one bucket.
+@pytest.mark.parametrize("R,E", [(0, 4), (1, 1), (255, 8), (256, 8), (257, 8), (1000, 1), (2048, 8), (2049, 8),
+                                 (2048, 256), (4096, 255), (4096, 256), (4097, 256),
                                  (2048, 257), (4097, 128), (6000, 9), (8192, 128), (8192, 1), (8193, 128),
                                  (8192, 129), (5000, 256), (32768, 256), (40000, 4096), (300000, 64)])
 @pytest.mark.parametrize("idt", [torch.int32, torch.int64])

@@ -166,18 +166,56 @@ __global__ __launch_bounds__(kScanThreads) void route_tiles_kernel(const int32_t
   build_tile_table(s_off, E, bm, wsum, tile_expert, tile_mstart, meta);
 }
 
-template <typename IdxT>
+// SCAN = false: blockoff holds route_scan_kernel's per-chunk prefixes and
+// offsets the segment starts.  SCAN = true (E + 1 <= kRouteThreads, so the
+// scan needs no launch of its own): blockoff holds route_count_kernel's raw
+// per-chunk counts, from which every workgroup derives the segment starts
+// and its chunk's prefixes, and workgroup 0 writes counts, offsets and the
+// tile table as route_scan_kernel does.
+template <typename IdxT, bool SCAN>
 __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
     const IdxT* __restrict__ ids, int64_t R, int64_t R_ids, int E_ids, int E, int chunk, int nb,
-    const int32_t* __restrict__ blockoff, const int32_t* __restrict__ offsets,
-    int32_t* __restrict__ sorted_rows) {
-  extern __shared__ int32_t sm[];  // base[E+1], wcnt[4][E+1]
+    const int32_t* __restrict__ blockoff, int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_rows,
+    int32_t* __restrict__ counts, int bm, int32_t* __restrict__ tile_expert, int32_t* __restrict__ tile_mstart,
+    int32_t* __restrict__ meta) {
+  extern __shared__ int32_t sm[];  // base[E+1], wcnt[4][E+1]; SCAN: s_off[E+2], wsum[4]
   constexpr int NW = kRouteThreads / kWave;
   int32_t* base = sm;
   int32_t* wcnt = sm + (E + 1);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int nbits = 32 - __clz(E);  // bucket values lie in [0, E]
-  for (int e = tid; e <= E; e += kRouteThreads) base[e] = offsets[e] + blockoff[(int64_t)e * nb + blockIdx.x];
+  if constexpr (SCAN) {
+    int32_t* s_off = wcnt + NW * (E + 1);
+    int32_t* wsum = s_off + (E + 2);
+    int32_t tot = 0, pre = 0;
+    if (tid <= E) {
+      const int32_t* row = blockoff + (int64_t)tid * nb;
+#pragma unroll 8
+      for (int b = 0; b < nb; ++b) {
+        const int32_t c = row[b];
+        tot += c;
+        pre += b < (int)blockIdx.x ? c : 0;
+      }
+    }
+    const int32_t start = block_excl_scan(tot, wsum);
+    if (tid <= E) {
+      base[tid] = start + pre;
+      s_off[tid] = start;
+    }
+    if (blockIdx.x == 0) {
+      if (tid <= E) {
+        offsets[tid] = start;
+        if (tid < E) counts[tid] = tot;
+      }
+      if (tid == 0) s_off[E + 1] = (int32_t)R;
+      if (bm > 0) {
+        __syncthreads();
+        build_tile_table(s_off, E, bm, wsum, tile_expert, tile_mstart, meta);
+      }
+    }
+  } else {
+    for (int e = tid; e <= E; e += kRouteThreads) base[e] = offsets[e] + blockoff[(int64_t)e * nb + blockIdx.x];
+  }
   const int64_t lo = (int64_t)blockIdx.x * chunk;
   const int64_t hi = std::min<int64_t>(R, lo + chunk);
   const uint64_t lt_mask = (1ull << lane) - 1ull;
@@ -522,7 +560,9 @@ template <typename IdxT>
 static int launch_route(const IdxT* ids, int64_t R, int64_t R_ids, int E_ids, int E, int32_t* blockcnt,
                         int32_t* counts, int32_t* offsets, int32_t* sorted_rows, int bm, int32_t* tile_expert,
                         int32_t* tile_mstart, int32_t* meta, hipStream_t st) {
-  if (R <= kRouteSmallRows && E <= kRouteSmallE) {
+  // One workgroup up to 2048 rows; beyond that the count + scatter pair is
+  // faster (measured), unless E + 1 buckets need route_scan_kernel as well.
+  if (E <= kRouteSmallE && (R <= 2048 || (R <= kRouteSmallRows && E + 1 > kRouteThreads))) {
     route_small_kernel<IdxT><<<1, kRouteSmallThreads, 0, st>>>(ids, R, R_ids, E_ids, E, counts, offsets, sorted_rows, bm,
                                                           tile_expert, tile_mstart, meta);
     return check_launch("route_small_kernel");
@@ -531,19 +571,27 @@ static int launch_route(const IdxT* ids, int64_t R, int64_t R_ids, int E_ids, in
   const size_t hist_lds = (size_t)(E + 1) * sizeof(int32_t);
   route_count_kernel<IdxT><<<p.nb, kRouteThreads, hist_lds, st>>>(ids, R, R_ids, E_ids, E, p.chunk, p.nb, blockcnt);
   if (int rc = check_launch("route_count_kernel")) return rc;
+  const size_t scat_lds = (size_t)(E + 1) * (1 + kRouteThreads / kWave) * sizeof(int32_t);
+  if (E + 1 <= kRouteThreads) {
+    // Few buckets: each scatter workgroup scans the count table itself.
+    const size_t lds = scat_lds + (size_t)(E + 2 + kRouteThreads / kWave) * sizeof(int32_t);
+    route_scatter_kernel<IdxT, true><<<p.nb, kRouteThreads, lds, st>>>(
+        ids, R, R_ids, E_ids, E, p.chunk, p.nb, blockcnt, offsets, sorted_rows, counts, bm, tile_expert, tile_mstart,
+        meta);
+    return check_launch("route_scatter_kernel");
+  }
   route_scan_kernel<<<1, kScanThreads, 0, st>>>(blockcnt, R, E, p.nb, counts, offsets, bm, tile_expert,
                                                  tile_mstart, meta);
   if (int rc = check_launch("route_scan_kernel")) return rc;
-  const size_t scat_lds = (size_t)(E + 1) * (1 + kRouteThreads / kWave) * sizeof(int32_t);
   static bool attr_set = false;  // E = 4096 needs more than the default 64 KB
   if (!attr_set) {
-    MOE_HIP_CHECK(hipFuncSetAttribute((const void*)route_scatter_kernel<IdxT>,
+    MOE_HIP_CHECK(hipFuncSetAttribute((const void*)route_scatter_kernel<IdxT, false>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
                                       (int)((kMaxExperts + 1) * (1 + kRouteThreads / kWave) * sizeof(int32_t))));
     attr_set = true;
   }
-  route_scatter_kernel<IdxT><<<p.nb, kRouteThreads, scat_lds, st>>>(ids, R, R_ids, E_ids, E, p.chunk, p.nb,
-                                                                     blockcnt, offsets, sorted_rows);
+  route_scatter_kernel<IdxT, false><<<p.nb, kRouteThreads, scat_lds, st>>>(
+      ids, R, R_ids, E_ids, E, p.chunk, p.nb, blockcnt, offsets, sorted_rows, nullptr, 0, nullptr, nullptr, nullptr);
   return check_launch("route_scatter_kernel");
 }
 
