@@ -142,9 +142,13 @@ def torch_moe_ref(x, w, k, wts, ids):
 
 # (4096, 4096, 256, 256, 8, 2): the up GEMM takes 64-row tiles and the down
 # GEMM 256-row tiles, so the down GEMM rebuilds the tile table from the up
-# GEMM's routing.
+# GEMM's routing.  (1024, ..., 8, 2) (Small-Test) and (1500, ..., 1): at most
+# 2048 routed rows but more than 2048 with the shared expert's appended rows,
+# sorted by the one-workgroup routing sort with the appended rows placed
+# directly.
 @pytest.mark.parametrize("T,Dh,De,Ds,E,k", [(2048, 2048, 1024, 1024, 8, 4), (4096, 1024, 512, 0, 64, 6),
-                                            (4096, 4096, 256, 256, 8, 2)])
+                                            (4096, 4096, 256, 256, 8, 2), (1024, 2048, 512, 512, 8, 2),
+                                            (1500, 512, 256, 256, 8, 1)])
 def test_fusedmoe_large(cuda, T, Dh, De, Ds, E, k):
     x, w = _moe_weights(T, Dh, De, Ds, E, seed=T)
     out, wts, ids = K.fused_moe_routed(x, **w, n_experts_per_token=k, return_routing=True)
