@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <atomic>
 #include <string>
 
 #include "../../include/moe_hip.h"
@@ -24,6 +26,21 @@ int check_launch(const char* what);
       return ::moe::fail(MOE_EHIP, std::string(#expr) + ": " +                 \
                                        hipGetErrorString(_e));                 \
   } while (0)
+
+// Raises a kernel's dynamic-LDS limit to `bytes` once per device.  `done`
+// is the call site's static mask of devices already set (device d < 64 is
+// bit d); concurrent first calls may both set the attribute, which is
+// harmless.  Returns 0 or a hipError_t.
+inline hipError_t lds_cap_once(std::atomic<uint64_t>& done, const void* kernel, int bytes) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
+  return e;
+}
 
 // Top-K + softmax of the rows sum_g part[g][M][N], g in order 0..G-1 (fp32
 // partials of a split-H router GEMM), N <= 256; one wave per row.

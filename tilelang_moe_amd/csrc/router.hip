@@ -1408,13 +1408,9 @@ template <typename T, typename IdxT, int VEC, int KPT>
 static int launch_radix_reg(const T* x, int64_t M, int N, int64_t ld, int K, float* s, IdxT* id,
                             hipStream_t st) {
   const int Kpad = next_pow2(K);
-  static bool attr_set = false;
-  if (!attr_set) {
-    MOE_HIP_CHECK(hipFuncSetAttribute((const void*)topk_radix_reg_kernel<T, IdxT, VEC, KPT>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)(kRadixDynLds)));
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_cap_set{0};
+  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)topk_radix_reg_kernel<T, IdxT, VEC, KPT>,
+                              (int)(kRadixDynLds)));
   topk_radix_reg_kernel<T, IdxT, VEC, KPT><<<dim3((unsigned)M), dim3(kRadixThreads),
                                               kRadixDynLds, st>>>(x, M, N, ld, K, Kpad,
                                                                                      s, id);
@@ -1484,13 +1480,9 @@ static size_t split_ws_bytes(int64_t M) {
 template <typename T, typename IdxT, int VEC, int KPT>
 static int launch_radix_split(const T* x, int64_t M, int N, int64_t ld, int K, int G, int slice, float* s,
                               IdxT* id, void* ws, hipStream_t st) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    MOE_HIP_CHECK(hipFuncSetAttribute((const void*)topk_radix_split_kernel<T, IdxT, VEC, KPT>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)(kRadixDynLds)));
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_cap_set{0};
+  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)topk_radix_split_kernel<T, IdxT, VEC, KPT>,
+                              (int)(kRadixDynLds)));
   SplitRowCtl* ctl = static_cast<SplitRowCtl*>(ws);
   uint64_t* gcand = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + kWsCtlBytes);
   const int64_t grid = (M + 7) / 8 * 8 * G;
@@ -1527,13 +1519,9 @@ static int launch_radix(const T* x, int64_t M, int64_t N, int64_t ld, int K, flo
   }
   const int Kpad = next_pow2(K);
   const size_t lds = (size_t)Kpad * sizeof(uint64_t);
-  static bool attr_set = false;  // raise the dynamic-LDS cap once per process
-  if (!attr_set) {
-    MOE_HIP_CHECK(hipFuncSetAttribute((const void*)topk_radix_kernel<T, IdxT>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)(kRadixMaxK * sizeof(uint64_t))));
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_cap_set{0};  // raise the dynamic-LDS cap once per device
+  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)topk_radix_kernel<T, IdxT>,
+                              (int)(kRadixMaxK * sizeof(uint64_t))));
   topk_radix_kernel<T, IdxT><<<dim3((unsigned)M), dim3(kRadixThreads), lds, st>>>(x, M, N, ld, K,
                                                                                Kpad, s, id);
   return check_launch("topk_radix_kernel");

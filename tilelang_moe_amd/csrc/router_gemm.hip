@@ -284,12 +284,8 @@ static size_t router_ws_bytes(const RouterPlan& p, int64_t T, int64_t E) {
 template <typename T, typename Cfg, int EPI, typename IdxT>
 static int launch_router(const RouterPlan& p, const uint16_t* x, const uint16_t* wt, int64_t Tn, int64_t H,
                          int E, int K, float* logits, float* scores, IdxT* idx, void* ws, hipStream_t st) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    MOE_HIP_CHECK(hipFuncSetAttribute((const void*)router_gemm_kernel<T, Cfg, EPI, IdxT>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cfg::LDS_BYTES));
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_cap_set{0};
+  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)router_gemm_kernel<T, Cfg, EPI, IdxT>, (int)Cfg::LDS_BYTES));
   float* part = p.G > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kWsCtlBytes) : nullptr;
   const int64_t grid = p.tiles * p.G;
   router_gemm_kernel<T, Cfg, EPI, IdxT><<<dim3((unsigned)grid), Cfg::THREADS, Cfg::LDS_BYTES, st>>>(
