@@ -27,17 +27,25 @@ int check_launch(const char* what);
                                        hipGetErrorString(_e));                 \
   } while (0)
 
-// Raises a kernel's dynamic-LDS limit to `bytes` once per device.  `done`
-// is the call site's static mask of devices already set (device d < 64 is
-// bit d); concurrent first calls may both set the attribute, which is
-// harmless.  Returns 0 or a hipError_t.
-inline hipError_t lds_cap_once(std::atomic<uint64_t>& done, const void* kernel, int bytes) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+// Raises a kernel's dynamic-LDS limit to `bytes` once per device, on the
+// device of the launch stream `st` (made current for the call if it is not).
+// `done` is the call site's static mask of devices already set (device d <
+// 64 is bit d); concurrent first calls may both set the attribute, which is
+// harmless.  Returns hipSuccess or the failing call's error.
+inline hipError_t lds_cap_once(std::atomic<uint64_t>& done, const void* kernel, int bytes, hipStream_t st) {
+  hipDevice_t dev = 0;
+  hipError_t e = hipStreamGetDevice(st, &dev);
   if (e != hipSuccess) return e;
   const uint64_t bit = 1ull << (dev & 63);
   if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+  int cur = 0;
+  if ((e = hipGetDevice(&cur)) != hipSuccess) return e;
+  if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
   e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (cur != dev) {
+    const hipError_t r = hipSetDevice(cur);
+    if (e == hipSuccess) e = r;
+  }
   if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
   return e;
 }

@@ -585,7 +585,7 @@ static int launch_route(const IdxT* ids, int64_t R, int64_t R_ids, int E_ids, in
   if (int rc = check_launch("route_scan_kernel")) return rc;
   static std::atomic<uint64_t> lds_cap_set{0};  // E = 4096 needs more than the default 64 KB
   MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)route_scatter_kernel<IdxT, false>,
-                              (int)((kMaxExperts + 1) * (1 + kRouteThreads / kWave) * sizeof(int32_t))));
+                              (int)((kMaxExperts + 1) * (1 + kRouteThreads / kWave) * sizeof(int32_t)), st));
   route_scatter_kernel<IdxT, false><<<p.nb, kRouteThreads, scat_lds, st>>>(
       ids, R, R_ids, E_ids, E, p.chunk, p.nb, blockcnt, offsets, sorted_rows, nullptr, 0, nullptr, nullptr, nullptr);
   return check_launch("route_scatter_kernel");
@@ -597,7 +597,7 @@ static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, con
                        int64_t R_ids, int E_ids, int64_t x_shift, const int32_t* sorted, const int32_t* offsets,
                        const int32_t* t_exp, const int32_t* t_ms, const int32_t* meta) {
   static std::atomic<uint64_t> lds_cap_set{0};
-  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_kernel<T, Cfg, MODE, EPI>, (int)Cfg::LDS_BYTES));
+  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_kernel<T, Cfg, MODE, EPI>, (int)Cfg::LDS_BYTES, st));
   // Persistent grid of SUPER workgroups per XCD (8 XCDs x 32 CUs x MINB) when
   // the tile list can be long; otherwise one workgroup per possible tile.
   const int64_t ub = ((R + Cfg::BM - 1) / Cfg::BM + E + 1) * ntn;  // tiles, upper bound

@@ -1410,7 +1410,7 @@ static int launch_radix_reg(const T* x, int64_t M, int N, int64_t ld, int K, flo
   const int Kpad = next_pow2(K);
   static std::atomic<uint64_t> lds_cap_set{0};
   MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)topk_radix_reg_kernel<T, IdxT, VEC, KPT>,
-                              (int)(kRadixDynLds)));
+                              (int)(kRadixDynLds), st));
   topk_radix_reg_kernel<T, IdxT, VEC, KPT><<<dim3((unsigned)M), dim3(kRadixThreads),
                                               kRadixDynLds, st>>>(x, M, N, ld, K, Kpad,
                                                                                      s, id);
@@ -1482,7 +1482,7 @@ static int launch_radix_split(const T* x, int64_t M, int N, int64_t ld, int K, i
                               IdxT* id, void* ws, hipStream_t st) {
   static std::atomic<uint64_t> lds_cap_set{0};
   MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)topk_radix_split_kernel<T, IdxT, VEC, KPT>,
-                              (int)(kRadixDynLds)));
+                              (int)(kRadixDynLds), st));
   SplitRowCtl* ctl = static_cast<SplitRowCtl*>(ws);
   uint64_t* gcand = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + kWsCtlBytes);
   const int64_t grid = (M + 7) / 8 * 8 * G;
@@ -1521,7 +1521,7 @@ static int launch_radix(const T* x, int64_t M, int64_t N, int64_t ld, int K, flo
   const size_t lds = (size_t)Kpad * sizeof(uint64_t);
   static std::atomic<uint64_t> lds_cap_set{0};  // raise the dynamic-LDS cap once per device
   MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)topk_radix_kernel<T, IdxT>,
-                              (int)(kRadixMaxK * sizeof(uint64_t))));
+                              (int)(kRadixMaxK * sizeof(uint64_t)), st));
   topk_radix_kernel<T, IdxT><<<dim3((unsigned)M), dim3(kRadixThreads), lds, st>>>(x, M, N, ld, K,
                                                                                Kpad, s, id);
   return check_launch("topk_radix_kernel");

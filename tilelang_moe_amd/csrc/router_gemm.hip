@@ -285,7 +285,7 @@ template <typename T, typename Cfg, int EPI, typename IdxT>
 static int launch_router(const RouterPlan& p, const uint16_t* x, const uint16_t* wt, int64_t Tn, int64_t H,
                          int E, int K, float* logits, float* scores, IdxT* idx, void* ws, hipStream_t st) {
   static std::atomic<uint64_t> lds_cap_set{0};
-  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)router_gemm_kernel<T, Cfg, EPI, IdxT>, (int)Cfg::LDS_BYTES));
+  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)router_gemm_kernel<T, Cfg, EPI, IdxT>, (int)Cfg::LDS_BYTES, st));
   float* part = p.G > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kWsCtlBytes) : nullptr;
   const int64_t grid = p.tiles * p.G;
   router_gemm_kernel<T, Cfg, EPI, IdxT><<<dim3((unsigned)grid), Cfg::THREADS, Cfg::LDS_BYTES, st>>>(
