@@ -181,3 +181,33 @@ def test_empty_and_repeated_calls(cuda):
     for T in (8, 200, 8, 64):
         X, W = make(T, 4096, 128, seed=T)
         check_fused(X, W, 8)
+
+
+def test_strided_weight_view(cuda):
+    """W given as a transposed view (unit row stride, column stride H): the
+    wrappers make it unit-column-stride before the transpose kernel reads it."""
+    g = torch.Generator(device="cuda").manual_seed(7)
+    T, H, E, k = 96, 512, 48, 6
+    X = torch.randn(T, H, generator=g, device="cuda").bfloat16()
+    Wt_full = (torch.randn(E, H, generator=g, device="cuda") / H ** 0.5).bfloat16()
+    W_view = Wt_full.t()  # [H, E], stride (1, H)
+    assert W_view.stride(1) != 1
+    W = W_view.contiguous()
+    for a, b in zip(K.router_topk_softmax(X, W_view, k), K.router_topk_softmax(X, W, k)):
+        assert torch.equal(a, b)
+    assert torch.equal(K.router_gemm(X, W_view), K.router_gemm(X, W))
+
+
+@pytest.mark.parametrize("E,k", [(64, 8), (300, 4)])  # fused kernel; beyond the fused limit (two launches)
+def test_prepared_weight_matches(cuda, E, k):
+    g = torch.Generator(device="cuda").manual_seed(E)
+    T, H = 200, 1024
+    X = torch.randn(T, H, generator=g, device="cuda").bfloat16()
+    W = (torch.randn(H, E, generator=g, device="cuda") / H ** 0.5).bfloat16()
+    Wt = K.prepare_router_weight(W)
+    assert Wt.shape == (E, H) and Wt.is_contiguous()
+    assert torch.equal(Wt, W.t().contiguous())
+    for a, b in zip(K.router_topk_softmax_prepared(X, Wt, k), K.router_topk_softmax(X, W, k)):
+        assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        K.router_topk_softmax_prepared(X, W, k)  # [H, E] is not a prepared [E, H] weight

@@ -40,8 +40,10 @@ from .fusedmoe import (
 from .router_gemm_topk_softmax import (
     get_fused_router_kernel,
     get_router_gemm_kernel,
+    prepare_router_weight,
     router_gemm,
     router_topk_softmax,
+    router_topk_softmax_prepared,
 )
 
 __all__ = [
@@ -65,6 +67,8 @@ __all__ = [
     "route_sort",
     "router_gemm",
     "router_topk_softmax",
+    "prepare_router_weight",
+    "router_topk_softmax_prepared",
     "get_router_gemm_kernel",
     "get_fused_router_kernel",
     "fusedmoe",

@@ -76,19 +76,30 @@ _WT_CACHE_MAX = 16
 
 def transposed_weight(W: torch.Tensor, E: int) -> torch.Tensor:
     """Wt [E, H] (contiguous) from W [H, >=E] (row stride >= E, unit column
-    stride), computed on the device and cached per weight tensor."""
+    stride), computed on the device and cached per weight tensor.
+
+    The cache key includes torch's version counter of W, so an eager call
+    after an in-place update of W transposes again.  A captured HIP graph
+    cannot consult that counter at replay, so while the current stream is
+    capturing, the transpose is always recorded into the graph (and not
+    cached): every replay then reads W as it is at replay time, as the
+    reference's kernels do."""
     H = W.shape[0]
+    capturing = torch.cuda.is_current_stream_capturing()
     key = (W.device.index, W.untyped_storage().data_ptr(), W.storage_offset(), W._version,
            tuple(W.shape), tuple(W.stride()), W.dtype, E)
-    with _wt_lock:
-        hit = _wt_cache.get(key)
-        if hit is not None:
-            _wt_cache.move_to_end(key)
-            return hit[1]
+    if not capturing:
+        with _wt_lock:
+            hit = _wt_cache.get(key)
+            if hit is not None:
+                _wt_cache.move_to_end(key)
+                return hit[1]
     Wt = torch.empty((E, H), dtype=W.dtype, device=W.device)
     L = _lib.lib()
     _lib.check(L.moe_router_weight_transpose(W.data_ptr(), _DTYPES[W.dtype], H, E, W.stride(0),
                                              Wt.data_ptr(), _lib.current_stream(W.device)))
+    if capturing:
+        return Wt
     with _wt_lock:
         _wt_cache[key] = (W, Wt)  # W is held so its storage cannot be reused under this key
         while len(_wt_cache) > _WT_CACHE_MAX:
@@ -96,7 +107,9 @@ def transposed_weight(W: torch.Tensor, E: int) -> torch.Tensor:
     return Wt
 
 
-def _check(X: torch.Tensor, W: torch.Tensor, E: int) -> Tuple[torch.Tensor, int, int]:
+def _check(X: torch.Tensor, W: torch.Tensor, E: int) -> Tuple[torch.Tensor, torch.Tensor, int, int]:
+    """Validates X [T, H] and W [H, >=E]; returns (X, W, T, H) with X
+    contiguous and W of unit column stride (what the transpose reads)."""
     if not isinstance(X, torch.Tensor) or not isinstance(W, torch.Tensor):
         raise TypeError("X and W must be torch.Tensors")
     if X.dim() != 2 or W.dim() != 2:
@@ -113,14 +126,94 @@ def _check(X: torch.Tensor, W: torch.Tensor, E: int) -> Tuple[torch.Tensor, int,
     if W.stride(1) != 1:
         W = W.contiguous()
     X = X.contiguous()
-    return X, T, H
+    return X, W, T, H
+
+
+def prepare_router_weight(W: torch.Tensor, E: int = None) -> torch.Tensor:
+    """The router weight in the kernels' layout, Wt [E, H] (K-contiguous rows,
+    the MFMA B operand), from W [H, >=E].  For callers that prepare weights
+    once at load time and call router_topk_softmax_prepared, e.g. from a
+    replayed HIP graph, so that no transpose runs per call.  Not cached: the
+    result is a snapshot of W."""
+    E = W.shape[1] if E is None else int(E)
+    _, W, _, H = _check(W.new_empty((0, W.shape[0])), W, E)
+    Wt = torch.empty((E, H), dtype=W.dtype, device=W.device)
+    _lib.check(_lib.lib().moe_router_weight_transpose(W.data_ptr(), _DTYPES[W.dtype], H, E, W.stride(0),
+                                                      Wt.data_ptr(), _lib.current_stream(W.device)))
+    return Wt
+
+
+def _check_prepared(X: torch.Tensor, Wt: torch.Tensor) -> Tuple[torch.Tensor, int, int, int]:
+    if not isinstance(X, torch.Tensor) or not isinstance(Wt, torch.Tensor):
+        raise TypeError("X and Wt must be torch.Tensors")
+    if X.dim() != 2 or Wt.dim() != 2:
+        raise ValueError(f"expected X [T, H] and Wt [E, H], got {tuple(X.shape)} and {tuple(Wt.shape)}")
+    if not Wt.is_contiguous():
+        raise ValueError("Wt must be contiguous [E, H] (prepare_router_weight returns it so)")
+    if X.device.type != "cuda" or Wt.device != X.device:
+        raise ValueError("the router runs on the GPU only: X and Wt must be cuda (HIP) tensors on one device")
+    if X.dtype not in _DTYPES or Wt.dtype != X.dtype:
+        raise ValueError(f"X and Wt must both be bfloat16 or both float16, got {X.dtype} and {Wt.dtype}")
+    T, H = X.shape
+    E = Wt.shape[0]
+    if Wt.shape[1] != H or E < 1:
+        raise ValueError(f"hidden size mismatch: X has H={H}, Wt is {tuple(Wt.shape)}")
+    return X.contiguous(), T, H, E
+
+
+def _router_gemm_wt(X: torch.Tensor, Wt: torch.Tensor, T: int, H: int, E: int) -> torch.Tensor:
+    logits = torch.empty((T, E), dtype=torch.float32, device=X.device)
+    if T == 0:
+        return logits
+    L = _lib.lib()
+    stream = _lib.current_stream(X.device)
+    ws_bytes = L.moe_router_workspace_size(T, H, E)
+    ws = _lib.workspace(X.device, stream, ws_bytes)
+    _lib.check(L.moe_router_gemm(X.data_ptr(), Wt.data_ptr(), _DTYPES[X.dtype], T, H, E, logits.data_ptr(),
+                                 ws.data_ptr(), ws_bytes, stream))
+    return logits
+
+
+def _router_topk_wt(X: torch.Tensor, Wt: torch.Tensor, T: int, H: int, E: int, k: int,
+                    index_dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+    k = int(k)
+    if not 1 <= k <= E:
+        raise ValueError(f"k must satisfy 1 <= k <= E={E}, got {k}")
+    if index_dtype not in (torch.int32, torch.int64):
+        raise ValueError("index_dtype must be torch.int32 or torch.int64")
+    if E > FUSED_MAX_E or k > FUSED_MAX_K:
+        logits = _router_gemm_wt(X, Wt, T, H, E)
+        if index_dtype == torch.int64:
+            return topk_softmax_int64(logits, k)
+        return topk_softmax(logits, k)
+    scores = torch.empty((T, k), dtype=torch.float32, device=X.device)
+    indices = torch.empty((T, k), dtype=index_dtype, device=X.device)
+    if T == 0:
+        return scores, indices
+    L = _lib.lib()
+    stream = _lib.current_stream(X.device)
+    ws_bytes = L.moe_router_workspace_size(T, H, E)
+    ws = _lib.workspace(X.device, stream, ws_bytes)
+    _lib.check(L.moe_router_topk_softmax(X.data_ptr(), Wt.data_ptr(), _DTYPES[X.dtype], T, H, E, k,
+                                         scores.data_ptr(), indices.data_ptr(),
+                                         _lib.MOE_I64 if index_dtype == torch.int64 else _lib.MOE_I32,
+                                         ws.data_ptr(), ws_bytes, stream))
+    return scores, indices
+
+
+def router_topk_softmax_prepared(X: torch.Tensor, Wt: torch.Tensor, k: int,
+                                 index_dtype: torch.dtype = torch.int32) -> Tuple[torch.Tensor, torch.Tensor]:
+    """router_topk_softmax with the weight already in the kernels' layout
+    (Wt [E, H] from prepare_router_weight): no transpose, no cache lookup."""
+    X, T, H, E = _check_prepared(X, Wt)
+    return _router_topk_wt(X, Wt, T, H, E, k, index_dtype)
 
 
 def router_gemm(X: torch.Tensor, W: torch.Tensor, E: int = None) -> torch.Tensor:
     """logits fp32 [T, E] = X [T, H] @ W [H, E] (W may carry padding columns
     past E)."""
     E = W.shape[1] if E is None else int(E)
-    X, T, H = _check(X, W, E)
+    X, W, T, H = _check(X, W, E)
     logits = torch.empty((T, E), dtype=torch.float32, device=X.device)
     if T == 0:
         return logits
@@ -139,31 +232,20 @@ def router_topk_softmax(X: torch.Tensor, W: torch.Tensor, k: int, E: int = None,
     """(scores fp32 [T, k], indices [T, k]) of softmax(top-k(X @ W)) per token,
     fused in one kernel (logits stay in LDS) when E <= 256 and k <= 32."""
     E = W.shape[1] if E is None else int(E)
-    X, T, H = _check(X, W, E)
+    X, W, T, H = _check(X, W, E)
     k = int(k)
     if not 1 <= k <= E:
         raise ValueError(f"k must satisfy 1 <= k <= E={E}, got {k}")
-    if index_dtype not in (torch.int32, torch.int64):
-        raise ValueError("index_dtype must be torch.int32 or torch.int64")
     if E > FUSED_MAX_E or k > FUSED_MAX_K:
+        # Validated first, like the fused path; router_gemm transposes itself.
+        if index_dtype not in (torch.int32, torch.int64):
+            raise ValueError("index_dtype must be torch.int32 or torch.int64")
         logits = router_gemm(X, W, E)
         if index_dtype == torch.int64:
             return topk_softmax_int64(logits, k)
         return topk_softmax(logits, k)
-    scores = torch.empty((T, k), dtype=torch.float32, device=X.device)
-    indices = torch.empty((T, k), dtype=index_dtype, device=X.device)
-    if T == 0:
-        return scores, indices
-    Wt = transposed_weight(W, E)
-    L = _lib.lib()
-    stream = _lib.current_stream(X.device)
-    ws_bytes = L.moe_router_workspace_size(T, H, E)
-    ws = _lib.workspace(X.device, stream, ws_bytes)
-    _lib.check(L.moe_router_topk_softmax(X.data_ptr(), Wt.data_ptr(), _DTYPES[X.dtype], T, H, E, k,
-                                         scores.data_ptr(), indices.data_ptr(),
-                                         _lib.MOE_I64 if index_dtype == torch.int64 else _lib.MOE_I32,
-                                         ws.data_ptr(), ws_bytes, stream))
-    return scores, indices
+    Wt = transposed_weight(W, E) if T > 0 else None
+    return _router_topk_wt(X, Wt, T, H, E, k, index_dtype)
 
 
 # ---------------------------------------------------------------------------
