@@ -32,6 +32,10 @@ def _inputs(seed):
     d["ids"] = torch.randint(0, 8, (512, 2), generator=g, device="cuda")
     d["Xr"] = torch.randn(256, 2048, generator=g, device="cuda").bfloat16()
     d["Wr"] = (torch.randn(2048, 64, generator=g, device="cuda") / math.sqrt(2048)).bfloat16()
+    # A weight in the kernels' layout, made once (fixed across replays, as at load time).
+    g_fixed = torch.Generator(device="cuda").manual_seed(99)
+    W_fixed = (torch.randn(2048, 96, generator=g_fixed, device="cuda") / math.sqrt(2048)).bfloat16()
+    d["Wt"] = K.prepare_router_weight(W_fixed)
     T, Dh, De, E = 128, 256, 128, 8
     d["x"] = torch.randn(T, Dh, generator=g, device="cuda").bfloat16()
     s = 1 / math.sqrt(Dh)
@@ -53,6 +57,7 @@ def _run_all(d):
     out += K.topk_softmax(d["sel"], 8)
     out.append(K.grouped_gemm(d["X"], d["W"], d["ids"]))
     out += K.router_topk_softmax(d["Xr"], d["Wr"], 8)
+    out += K.router_topk_softmax_prepared(d["Xr"], d["Wt"], 6)
     out.append(K.fused_moe_routed(d["x"], **d["moe"], n_experts_per_token=2))
     return out
 
@@ -93,6 +98,8 @@ def test_graph_replays_match_eager(cuda):
     for rep in range(3):
         fresh = _inputs(10 + rep)
         for key, t in fresh.items():
+            if key == "Wt":
+                continue  # prepared once, never updated
             if key == "moe":
                 for n, w in t.items():
                     d["moe"][n].copy_(w)
