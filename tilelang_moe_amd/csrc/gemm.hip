@@ -354,7 +354,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
     const int32_t* __restrict__ sorted_rows, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_mstart,
     const int32_t* __restrict__ meta) {
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, S = Cfg::STAGES, CPR = Cfg::CPR;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, CPR = Cfg::CPR;
   constexpr int OBN = EPI == 1 ? BN / 2 : BN;  // output columns per tile
   static_assert(EPI == 0 || Cfg::FN % 2 == 0, "SwiGLU pairs 32-column blocks within a wave");
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];  // [S][(BM+BN)*BK]

@@ -290,7 +290,6 @@ __global__ __launch_bounds__(256) void topk_select16_kernel(const uint16_t* __re
 // ===========================================================================
 constexpr int kRadixThreads = 1024;
 constexpr int kRadixBins = 2048;
-constexpr int kBuckets = 4096;
 constexpr int kBucketFixMax = 32;
 
 __device__ inline uint32_t block_excl_scan_1024(uint32_t v, uint32_t* wsum, uint32_t* total) {
