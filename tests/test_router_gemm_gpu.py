@@ -211,3 +211,13 @@ def test_prepared_weight_matches(cuda, E, k):
         assert torch.equal(a, b)
     with pytest.raises(ValueError):
         K.router_topk_softmax_prepared(X, W, k)  # [H, E] is not a prepared [E, H] weight
+
+
+@pytest.mark.parametrize("H,E", [(136, 72), (64, 8), (520, 300), (1000, 160), (7168, 256)])
+def test_weight_transpose_exact(cuda, H, E):
+    """prepare_router_weight is an exact transpose: 16-byte path (H, E
+    multiples of 8, partial 64x64 tiles included) and scalar path (E = 300)."""
+    W = torch.randn(H, E, device="cuda").bfloat16()
+    assert torch.equal(K.prepare_router_weight(W), W.t().contiguous())
+    Wpad = torch.randn(H, E + 8, device="cuda").bfloat16()  # padded columns past E (row stride E + 8)
+    assert torch.equal(K.prepare_router_weight(Wpad, E), Wpad[:, :E].t().contiguous())

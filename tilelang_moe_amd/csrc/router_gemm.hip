@@ -36,13 +36,42 @@
 namespace moe {
 
 // ---------------------------------------------------------------------------
-// Wt[E,H] = W[H,E]^T through a padded 64x64 LDS tile.
+// Wt[E,H] = W[H,E]^T through a padded 64x64 LDS tile (16-byte accesses when
+// rows are aligned and H, E are multiples of 8).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void router_transpose_kernel(const uint16_t* __restrict__ W,
                                                                uint16_t* __restrict__ Wt, int64_t H,
-                                                               int64_t E, int64_t ldw) {
-  __shared__ uint16_t tile[64][65];
+                                                               int64_t E, int64_t ldw, int vec) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][72];  // rows padded to 144 bytes
   const int64_t h0 = (int64_t)blockIdx.y * 64, e0 = (int64_t)blockIdx.x * 64;
+  if (vec) {
+    // 16-byte aligned rows and H, E multiples of 8 (vec), so every 8-column
+    // chunk lies wholly inside or outside the matrix: chunk c of the tile is
+    // row c / 8, columns 8 (c % 8) ..  Each thread moves two chunks in and
+    // two out; chunks past H or E are skipped (their LDS slots are unused).
+#pragma unroll
+    for (int c = threadIdx.x; c < 512; c += 256) {
+      const int r = c >> 3, q = c & 7;
+      if (h0 + r < H && e0 + 8 * q < E)
+        *reinterpret_cast<uint4*>(&tile[r][8 * q]) = *reinterpret_cast<const uint4*>(W + (h0 + r) * ldw + e0 + 8 * q);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = threadIdx.x; c < 512; c += 256) {
+      const int r = c >> 3, q = c & 7;  // output row e0 + r, columns h0 + 8q ..
+      if (e0 + r >= E || h0 + 8 * q >= H) continue;
+      uint16_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = tile[8 * q + j][r];
+      uint4 o;
+      o.x = v[0] | ((uint32_t)v[1] << 16);
+      o.y = v[2] | ((uint32_t)v[3] << 16);
+      o.z = v[4] | ((uint32_t)v[5] << 16);
+      o.w = v[6] | ((uint32_t)v[7] << 16);
+      *reinterpret_cast<uint4*>(Wt + (e0 + r) * H + h0 + 8 * q) = o;
+    }
+    return;
+  }
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   for (int r = ty; r < 64; r += 4) {
     const int64_t h = h0 + r, e = e0 + tx;
@@ -338,8 +367,10 @@ extern "C" int moe_router_weight_transpose(const void* W, int dtype, int64_t H, 
   if (!W || !Wt) return fail(MOE_EINVAL, "router_weight_transpose: null pointer");
   if ((H + 63) / 64 > 65535) return fail(MOE_EUNSUP, "router_weight_transpose: H too large");
   const dim3 grid((unsigned)((E + 63) / 64), (unsigned)((H + 63) / 64));
+  // 16-byte path: W and Wt rows 16-byte aligned, whole 8-column chunks.
+  const int vec = ((uintptr_t)W % 16 == 0) && ((uintptr_t)Wt % 16 == 0) && ldw % 8 == 0 && H % 8 == 0 && E % 8 == 0;
   router_transpose_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(W), static_cast<uint16_t*>(Wt), H, E, ldw);
+      static_cast<const uint16_t*>(W), static_cast<uint16_t*>(Wt), H, E, ldw, vec);
   return check_launch("router_transpose_kernel");
 }
 
