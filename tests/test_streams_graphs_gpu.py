@@ -111,3 +111,64 @@ def test_graph_replays_match_eager(cuda):
         want = _run_all(d)  # eager work between replays
         torch.cuda.synchronize()
         _assert_equal(static_out, want, f"replay {rep}")
+
+
+def test_capture_as_first_call_on_a_fresh_stream(cuda):
+    """Workspaces are never allocated inside a capture (they would belong to
+    the graph's private pool): a call that needs one raises with the warm-up
+    hint when it is the first call on the capturing stream, while calls that
+    need none capture and replay correctly as a fresh stream's first call."""
+    g = torch.Generator(device="cuda").manual_seed(5)
+    split = torch.randn(4, 65536, generator=g, device="cuda")   # split rows: needs a workspace
+    small = torch.randn(256, 64, generator=g, device="cuda").bfloat16()
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="warm-up"):
+        with torch.cuda.graph(graph, stream=s):
+            K.topk_softmax(split, 512)
+    torch.cuda.synchronize()
+    s2 = torch.cuda.Stream()
+    graph2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph2, stream=s2):
+        static_out = K.topk_softmax(small, 6)
+    for rep in range(3):
+        small.copy_(torch.randn(256, 64, generator=g, device="cuda").bfloat16())
+        torch.cuda.synchronize()
+        graph2.replay()
+        torch.cuda.synchronize()
+        _assert_equal(static_out, K.topk_softmax(small, 6), f"fresh-stream capture, replay {rep}")
+
+
+def test_graph_replay_after_workspace_growth(cuda):
+    """A graph captured on stream s keeps using the workspace it captured
+    after a larger eager call on s replaced that stream's workspace: the
+    replaced buffer stays alive, so replays neither read freed memory nor
+    race with tensors allocated since."""
+    g = torch.Generator(device="cuda").manual_seed(6)
+    x = torch.randn(4, 65536, generator=g, device="cuda")
+    big = torch.randn(200, 65536, generator=g, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        K.topk_softmax(x, 512)  # warm-up: the stream's workspace fits this call
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        static_out = K.topk_softmax(x, 512)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        want_big = K.topk_softmax(big, 512)  # grows the stream's workspace
+    torch.cuda.synchronize()
+    junk = [torch.full((1 << 20,), 0x7F, dtype=torch.uint8, device="cuda") for _ in range(16)]
+    for rep in range(3):
+        x.copy_(torch.randn(4, 65536, generator=g, device="cuda"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        _assert_equal(static_out, K.topk_softmax(x, 512), f"replay {rep} after growth")
+    with torch.cuda.stream(s):
+        again = K.topk_softmax(big, 512)
+    torch.cuda.synchronize()
+    _assert_equal(again, want_big, "eager call on the grown workspace")
+    del junk

@@ -9,6 +9,7 @@ from __future__ import annotations
 import os
 import shutil
 import subprocess
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -16,6 +17,11 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(REPO_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libmoe_hip.so")
+# Python binding of the two drop-in entry points (csrc/torch_bind.cpp):
+# host C++ against torch's C++ API, no HIP; it allocates the outputs in C++
+# and calls the library through addresses taken from ctypes.
+FAST_NAME = "_moe_torch"
+FAST_PATH = os.path.join(PKG_DIR, FAST_NAME + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 
 SOURCES = ["router.hip", "gemm.hip", "router_gemm.hip", "moe.hip", "capi.cpp"]
 ARCH = "gfx950"
@@ -54,8 +60,10 @@ def build(extra_flags: list[str] | None = None, verbose: bool = False) -> str:
     """Compile every source for gfx950 and link ``libmoe_hip.so``; returns its path."""
     extra = list(extra_flags or [])
     os.makedirs(BUILD_DIR, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+    with ThreadPoolExecutor(max_workers=len(SOURCES) + 1) as ex:
+        fast = ex.submit(build_fast)
         objs = list(ex.map(lambda s: _compile(s, extra), SOURCES))
+        fast.result()
     tmp = LIB_PATH + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
            "-Wl,-rpath,/opt/rocm/lib"]
@@ -64,8 +72,31 @@ def build(extra_flags: list[str] | None = None, verbose: bool = False) -> str:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
     if verbose:
-        print(f"built {LIB_PATH}")
+        print(f"built {LIB_PATH} and {FAST_PATH}")
     return LIB_PATH
+
+
+def build_fast() -> str:
+    """Compile the torch binding csrc/torch_bind.cpp in-tree with the host C++ compiler."""
+    import torch
+    from torch.utils import cpp_extension as ce
+
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no C++ compiler (g++) found for the torch binding")
+    abi = int(bool(getattr(torch._C, "_GLIBCXX_USE_CXX11_ABI", True)))
+    inc = [f"-I{p}" for p in ce.include_paths()] + [f"-I{sysconfig.get_paths()['include']}"]
+    libs = [f"-L{p}" for p in ce.library_paths()] + [f"-Wl,-rpath,{p}" for p in ce.library_paths()]
+    tmp = FAST_PATH + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-w", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           f"-DTORCH_EXTENSION_NAME={FAST_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H", *inc,
+           os.path.join(CSRC, "torch_bind.cpp"), "-o", tmp, *libs, "-lc10", "-ltorch", "-ltorch_cpu",
+           "-ltorch_python"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"building the torch binding failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, FAST_PATH)
+    return FAST_PATH
 
 
 if __name__ == "__main__":

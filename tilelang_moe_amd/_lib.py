@@ -12,7 +12,7 @@ import ctypes
 import os
 import threading
 
-from ._build import LIB_PATH
+from ._build import FAST_PATH, LIB_PATH
 
 MOE_F32, MOE_BF16, MOE_F16, MOE_I32, MOE_I64 = 0, 1, 2, 3, 4
 MOE_TOPK_AUTO, MOE_TOPK_BITONIC, MOE_TOPK_SELECTION, MOE_TOPK_RADIX = -1, 0, 1, 2
@@ -77,8 +77,28 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.restype = res
                 fn.argtypes = args
+            _bind_fast(handle)
             _lib = handle
     return _lib
+
+
+fast = None  # the torch binding (_moe_torch), bound by lib()
+
+
+def _bind_fast(handle) -> None:
+    """Hand the addresses of the two drop-in entry points to the torch
+    binding, which allocates their outputs in C++ and calls them with plain
+    integers (no ctypes conversion per call)."""
+    global fast
+    try:
+        from . import _moe_torch
+    except ImportError as e:
+        raise RuntimeError(f"the torch binding {FAST_PATH} is missing or stale ({e}): build with "
+                           "`python -m tilelang_moe_amd._build` (or __graft_entry__.build())") from e
+    addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value  # noqa: E731
+    _moe_torch.bind(addr(handle.moe_topk_softmax_ex), addr(handle.moe_grouped_gemm),
+                    addr(handle.moe_topk_softmax_workspace_size))
+    fast = _moe_torch
 
 
 def current_stream(dev) -> int:
@@ -93,29 +113,74 @@ def current_stream(dev) -> int:
     return torch.cuda.current_stream(idx).cuda_stream
 
 
-_ws_cache = {}
+_ws_cache = {}    # (device index, raw stream handle) -> (tensor, data_ptr, bytes)
+_ws_retired = []  # replaced buffers: a captured graph may still reference them
 _ws_lock = threading.Lock()
 
 
-def workspace(dev, stream: int, nbytes: int):
-    """Device workspace of at least `nbytes` for calls on (`dev`, `stream`).
+def workspace_ptr(dev_index: int, stream: int, nbytes: int) -> int:
+    """Device address of a zero-initialised workspace of at least `nbytes`
+    for calls on (`dev_index`, `stream`); 0 when nbytes is 0.
 
-    Calls on one stream are ordered, so they may share one buffer; calls on
-    different streams get different buffers.  The buffer only grows.  It is
-    zero-initialised once, as the C ABI requires."""
+    Calls on one stream are ordered, so they share one buffer; calls on
+    different streams get different buffers.  Every call leaves the
+    buffer's control block zero, so a buffer stays valid for the next call
+    on its stream, also when torch hands a stream handle to a new stream
+    (its streams live in pools and are never destroyed).
+
+    Buffers are made only outside graph capture: one allocated during
+    capture would belong to the graph's private memory pool.  A buffer that
+    is outgrown is replaced but kept alive (a graph captured earlier may
+    still use it).  Inside a capture the stream's existing buffer is used if
+    it is large enough; otherwise this raises, and the caller must make one
+    eager call of the same or a larger size on that stream before capture
+    (the usual warm-up)."""
+    if nbytes == 0:
+        return 0
+    ent = _ws_cache.get((dev_index, stream))
+    if ent is not None and ent[2] >= nbytes:
+        return ent[1]
+    return _grow(dev_index, stream, nbytes)[1]
+
+
+def _grow(dev_index: int, stream: int, nbytes: int):
     import torch
 
+    key = (dev_index, stream)
+    with _ws_lock:
+        ent = _ws_cache.get(key)
+        if ent is not None and ent[2] >= nbytes:
+            return ent
+        if torch.cuda.is_current_stream_capturing():
+            have = 0 if ent is None else ent[2]
+            raise RuntimeError(
+                f"tilelang_moe_amd: this call needs a {nbytes}-byte device workspace on the capturing stream, "
+                f"which has {have} bytes; workspaces are not allocated during graph capture. Run the same "
+                "call once eagerly on this stream before capturing (warm-up).")
+        size = max(nbytes, 1 << 16, 2 * (ent[2] if ent is not None else 0))
+        buf = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", dev_index))
+        if ent is not None:
+            _ws_retired.append(ent[0])
+        ent = (buf, buf.data_ptr(), size)
+        _ws_cache[key] = ent
+        return ent
+
+
+def workspace_entry(dev_index: int, stream: int):
+    """(data_ptr, bytes) of the current workspace of (dev_index, stream), or (0, 0)."""
+    ent = _ws_cache.get((dev_index, stream))
+    return (ent[1], ent[2]) if ent is not None else (0, 0)
+
+
+def workspace(dev, stream: int, nbytes: int):
+    """The workspace of workspace_ptr as a uint8 tensor (None when nbytes is 0)."""
     if nbytes == 0:
         return None
-    key = (dev.index, stream)
-    buf = _ws_cache.get(key)
-    if buf is None or buf.numel() < nbytes:
-        with _ws_lock:
-            buf = _ws_cache.get(key)
-            if buf is None or buf.numel() < nbytes:
-                buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
-                _ws_cache[key] = buf
-    return buf
+    idx = dev.index if dev.index is not None else __import__("torch").cuda.current_device()
+    ent = _ws_cache.get((idx, stream))
+    if ent is None or ent[2] < nbytes:
+        ent = _grow(idx, stream, nbytes)
+    return ent[0]
 
 
 def check(rc: int) -> None:

@@ -24,6 +24,9 @@ from .. import _lib
 
 _DTYPES = {torch.bfloat16: _lib.MOE_BF16, torch.float16: _lib.MOE_F16}
 _IDX = {torch.int32: _lib.MOE_I32, torch.int64: _lib.MOE_I64}
+_WS_SIZES = {}  # (T, topk, E, I) -> workspace bytes (the C ABI's answer, cached)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
+    lambda i: torch.cuda.current_stream(i).cuda_stream)
 
 
 def _check_ids(expert_indices: torch.Tensor, dev: torch.device) -> torch.Tensor:
@@ -72,16 +75,20 @@ def grouped_gemm(X: torch.Tensor, W: torch.Tensor, expert_indices: torch.Tensor)
     R = T * topk
     X = X.contiguous()
     W = W.contiguous()
-    Y = torch.empty((R, I), dtype=X.dtype, device=X.device)
-    if R == 0 or topk == 0:
-        return Y
     L = _lib.lib()
-    stream = _lib.current_stream(X.device)
-    ws_bytes = L.moe_grouped_gemm_workspace_size(T, topk, E, I)
-    ws = _lib.workspace(X.device, stream, ws_bytes)
-    _lib.check(L.moe_grouped_gemm(X.data_ptr(), W.data_ptr(), ids.data_ptr(), _DTYPES[X.dtype],
-                                  _IDX[ids.dtype], T, topk, H, I, E, Y.data_ptr(), ws.data_ptr(),
-                                  ws_bytes, stream))
+    didx = X.get_device()
+    stream = _raw_stream(didx)
+    key = (T, topk, E, I)
+    ws_bytes = _WS_SIZES.get(key)
+    if ws_bytes is None:
+        if len(_WS_SIZES) > 4096:
+            _WS_SIZES.clear()
+        ws_bytes = _WS_SIZES[key] = L.moe_grouped_gemm_workspace_size(T, topk, E, I) if R else 0
+    ws = _lib.workspace_ptr(didx, stream, ws_bytes)
+    rc, Y = _lib.fast.grouped_gemm(X, W, ids, _DTYPES[X.dtype], _IDX[ids.dtype], T, topk, H, I, E, ws,
+                                   ws_bytes, stream)
+    if rc:
+        _lib.check(rc)
     return Y
 
 

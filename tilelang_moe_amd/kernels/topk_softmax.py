@@ -23,8 +23,6 @@ import torch
 
 from .. import _lib
 
-_LOGIT_DTYPES = {torch.float32: _lib.MOE_F32, torch.bfloat16: _lib.MOE_BF16,
-                 torch.float16: _lib.MOE_F16}
 _IDX_DTYPES = {torch.int32: _lib.MOE_I32, torch.int64: _lib.MOE_I64}
 _ALGOS = {"auto": _lib.MOE_TOPK_AUTO, "bitonic": _lib.MOE_TOPK_BITONIC,
           "selection": _lib.MOE_TOPK_SELECTION, "radix": _lib.MOE_TOPK_RADIX}
@@ -41,43 +39,32 @@ def select_strategy(num_experts: int, k: int) -> str:
     return _ALGO_NAMES[_lib.lib().moe_topk_select_algo(int(num_experts), int(k))]
 
 
-def _check_logits(logits: torch.Tensor, k) -> Tuple[torch.Tensor, int]:
+_NEED_WORKSPACE = -100  # the binding's code for "workspace too small, nothing launched"
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
+    lambda i: torch.cuda.current_stream(i).cuda_stream)
+
+
+def _run(logits: torch.Tensor, k, algo: int, with_scores: bool,
+         index_dtype: torch.dtype = torch.int32, score_mode: int = _lib.MOE_SCORES_TOPK):
+    """One call of moe_topk_softmax_ex through the torch binding, which
+    checks the arguments (ValueError as in the reference), allocates the
+    outputs and launches on the current stream."""
     if not isinstance(logits, torch.Tensor):
         raise TypeError("logits must be a torch.Tensor")
-    if logits.dim() != 2:
-        raise ValueError(f"logits must be 2-D [num_tokens, num_experts], got shape {tuple(logits.shape)}")
-    if logits.dtype not in _LOGIT_DTYPES:
-        raise ValueError(f"logits dtype must be float32, bfloat16 or float16, got {logits.dtype}")
-    if logits.device.type != "cuda":
-        raise ValueError("topk_softmax runs on the GPU only: logits must be a cuda (HIP) tensor")
-    if isinstance(k, torch.Tensor):
-        k = int(k.item())
-    k = int(k)
-    n = logits.shape[1]
-    if not 1 <= k <= n:
-        raise ValueError(f"k must satisfy 1 <= k <= num_experts={n}, got {k}")
-    if logits.stride(1) != 1 or logits.stride(0) < n:
-        logits = logits.contiguous()
-    return logits, k
-
-
-def _run(logits: torch.Tensor, k: int, algo: int, with_scores: bool,
-         index_dtype: torch.dtype = torch.int32, score_mode: int = _lib.MOE_SCORES_TOPK):
-    logits, k = _check_logits(logits, k)
-    m, n = logits.shape
-    dev = logits.device
-    indices = torch.empty((m, k), dtype=index_dtype, device=dev)
-    scores = torch.empty((m, k), dtype=torch.float32, device=dev) if with_scores else None
-    if m == 0:
-        return scores, indices
-    L = _lib.lib()
-    stream = _lib.current_stream(dev)
-    ws_bytes = L.moe_topk_softmax_workspace_size(m, n, k, algo)
-    ws = _lib.workspace(dev, stream, ws_bytes)
-    _lib.check(L.moe_topk_softmax_ex(
-        logits.data_ptr(), _LOGIT_DTYPES[logits.dtype], m, n, logits.stride(0), k,
-        scores.data_ptr() if with_scores else None, indices.data_ptr(), _IDX_DTYPES[index_dtype],
-        algo, score_mode, ws.data_ptr() if ws is not None else None, ws_bytes, stream))
+    if k.__class__ is not int:
+        k = int(k.item()) if isinstance(k, torch.Tensor) else int(k)
+    fast = _lib.fast or (_lib.lib(), _lib.fast)[1]
+    didx = logits.get_device()
+    stream = _raw_stream(didx) if didx >= 0 else 0
+    ws, ws_bytes = _lib.workspace_entry(didx, stream)
+    rc, need, scores, indices = fast.topk_softmax(logits, k, algo, with_scores, index_dtype is torch.int64,
+                                                  score_mode, ws, ws_bytes, stream)
+    if rc == _NEED_WORKSPACE:
+        ws = _lib.workspace_ptr(didx, stream, need)
+        rc, need, scores, indices = fast.topk_softmax(logits, k, algo, with_scores, index_dtype is torch.int64,
+                                                      score_mode, ws, need, stream)
+    if rc:
+        _lib.check(rc)
     return scores, indices
 
 
