@@ -36,7 +36,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", default="", help="comma list of c1,c2,c3a,c3b,c4,c5,router,moe (profiling runs)")
+    p.add_argument("--only", default="", help="comma list of c1,c2,c3a,c3b,c4,c5,c5u,ep,router,moe (profiling runs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 1 GiB device-to-device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -200,49 +200,94 @@ def main():
         secondary[name] = entry
 
     # ---------------- grouped GEMM configs ----------------
-    def gemm_cfg(name, desc, T, H, I, E, topk, skew):
-        gg = torch.Generator().manual_seed(0)
-        if skew:
-            bias = 1.5 * torch.randn(E, generator=gg)
-            idx = torch.topk(torch.randn(T, E, generator=gg) + bias, topk).indices
-        else:
-            idx = torch.topk(torch.randn(T, E, generator=gg), topk).indices
+    # ms: the whole drop-in call (device routing sort + GEMM) by graph replay;
+    # ms_gemm: the GEMM alone on the routing the call before computed
+    # (grouped_gemm_reuse_routing), as the reference benchmark times its
+    # kernels with the routing done outside the timed region
+    # (benchmarks/benchmark_grouped_gemm.py:116-214).
+    def gemm_entry(desc, X, W, idx, topk, cpu_calls=0, cold=False):
+        T, H = X.shape
+        E, I, _ = W.shape
+        R = T * topk
+        calls, replays = (5, 4) if R * H * I > 1e11 else (20, 20)
+        ms_eager = gpu_time_ms(lambda: K.grouped_gemm(X, W, idx), max(5, min(args.steps, 50)),
+                               min(args.warmup, 5))
+        ms = graph_time_ms(lambda: K.grouped_gemm(X, W, idx), calls=calls, replays=replays)
+        K.grouped_gemm(X, W, idx)  # the routing tables the GEMM-only calls reuse
+        ms_gemm = gpu_time_ms(lambda: K.grouped_gemm_reuse_routing(X, W, topk), max(5, min(args.steps, 50)),
+                              min(args.warmup, 5))
+        flops = 2.0 * R * H * I
+        cnt = torch.bincount(idx.flatten(), minlength=E)
+        e_nz = int((cnt > 0).sum())
+        nbytes = e_nz * I * H * 2 + T * H * 2 + R * I * 2 + R * 4
+        tf = flops / ms / 1e9
+        entry = {"workload": desc, "ms": ms, "ms_eager": ms_eager, "ms_gemm": ms_gemm, "TFLOP_s": tf,
+                 "frac_mfma": tf / BF16_PEAK_TFLOPS, "TFLOP_s_gemm": flops / ms_gemm / 1e9,
+                 "GB_s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+                 "rows": R, "experts_nonempty": e_nz, "rows_max_expert": int(cnt.max()),
+                 "timing": "ms: HIP-graph replay of the whole call (routing sort + GEMM); ms_gemm: GEMM alone "
+                           "on reused routing tables, HIP events around back-to-back calls"}
+        if cold:
+            entry["ms_cold"] = cold_time_ms(lambda: K.grouped_gemm(X, W, idx))
+            entry["timing"] += "; ms_cold: one call after an L2/MALL flush, median of 50"
+        if cpu_calls and not args.no_cpu:
+            from oracle import torch_baseline as tb
+            Xc, Wc, ic = X.cpu(), W.cpu(), idx.cpu()
+            Xr = Xc.repeat_interleave(topk, 0) if topk > 1 else Xc
+            t_cpu = []
+            for _ in range(cpu_calls):
+                t0 = time.perf_counter()
+                tb.grouped_gemm_loop(Xr, Wc, ic.flatten())
+                t_cpu.append((time.perf_counter() - t0) * 1e3)
+            t_cpu.sort()
+            entry["cpu_ms"] = t_cpu[len(t_cpu) // 2]
+            entry["cpu_calls"] = cpu_calls
+            entry["cpu_threads"] = torch.get_num_threads()
+            del Xc, Wc, Xr
+        return entry
+
+    def gemm_weights(E, I, H):
         gc = torch.Generator(device=dev).manual_seed(0)
-        X = torch.randn(T, H, generator=gc, device=dev).bfloat16()
         W = torch.empty(E, I, H, dtype=torch.bfloat16, device=dev)
         for e0 in range(0, E, 32):
             e1 = min(E, e0 + 32)
             W[e0:e1] = (0.02 * torch.randn(e1 - e0, I, H, generator=gc, device=dev)).bfloat16()
-        idx = idx.to(dev)
-        steps = max(5, min(args.steps, 50 if skew else args.steps))
-        ms_eager = gpu_time_ms(lambda: K.grouped_gemm(X, W, idx), steps, min(args.warmup, 5))
-        ms = graph_time_ms(lambda: K.grouped_gemm(X, W, idx), calls=5 if skew else 20,
-                           replays=4 if skew else 20)
-        R = T * topk
-        flops = 2.0 * R * H * I
-        e_nz = int((torch.bincount(idx.flatten(), minlength=E) > 0).sum())
-        nbytes = e_nz * I * H * 2 + T * H * 2 + R * I * 2 + R * 4
-        tf = flops / ms / 1e9
-        secondary[name] = {"workload": desc, "ms": ms, "ms_eager": ms_eager, "TFLOP_s": tf,
-                           "frac_mfma": tf / BF16_PEAK_TFLOPS,
-                           "GB_s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS,
-                           "rows": R, "experts_nonempty": e_nz,
-                           "timing": "ms: HIP-graph replay of the whole call (routing sort + GEMM)"}
-        if not skew:
-            secondary[name]["ms_cold"] = cold_time_ms(lambda: K.grouped_gemm(X, W, idx))
-            secondary[name]["timing"] += "; ms_cold: one call after an L2/MALL flush, median of 50"
-        if not args.no_cpu and not skew:
-            from oracle import torch_baseline as tb
-            Xc, Wc, ic = X.cpu(), W.cpu(), idx.cpu()
-            secondary[name]["cpu_ms"] = cpu_time_ms(
-                lambda: tb.grouped_gemm_loop(Xc.repeat_interleave(topk, 0), Wc, ic.flatten()), 3.0)
-        del W, X
+        return W, gc
 
     if want("c4"):
-        gemm_cfg("c4", "grouped_gemm bf16 T=4096 H=1024 I=256 E=8 top-2 (8192 rows)", 4096, 1024, 256, 8, 2, False)
-    if want("c5"):
-        gemm_cfg("c5", "grouped_gemm bf16 T=4096 H=7168 I=2048 E=256 top-8 skewed (32768 rows)",
-                 4096, 7168, 2048, 256, 8, True)
+        gg = torch.Generator().manual_seed(0)
+        idx = torch.topk(torch.randn(4096, 8, generator=gg), 2).indices.to(dev)
+        W, gc = gemm_weights(8, 256, 1024)
+        X = torch.randn(4096, 1024, generator=gc, device=dev).bfloat16()
+        secondary["c4"] = gemm_entry("grouped_gemm bf16 T=4096 H=1024 I=256 E=8 top-2 (8192 rows)", X, W, idx, 2,
+                                     cpu_calls=5, cold=True)
+        del W, X
+    if want("c5") or want("c5u") or want("ep"):
+        W, gc = gemm_weights(256, 2048, 7168)
+        if want("c5"):
+            gg = torch.Generator().manual_seed(0)
+            bias = 1.5 * torch.randn(256, generator=gg)
+            idx = torch.topk(torch.randn(4096, 256, generator=gg) + bias, 8).indices.to(dev)
+            X = torch.randn(4096, 7168, generator=gc, device=dev).bfloat16()
+            secondary["c5"] = gemm_entry("grouped_gemm bf16 T=4096 H=7168 I=2048 E=256 top-8 skewed (32768 rows)",
+                                         X, W, idx, 8, cpu_calls=1)
+        # The reference benchmark's routing (benchmarks/benchmark_grouped_gemm.py:104-109):
+        # 4096 tokens * top-8 / 256 experts = 128 rows per expert, ids = arange % E_local
+        # over an X of that many rows; E_local = 256 (all experts) and the single-GPU
+        # expert-parallel shard E_local = 32.
+        if want("c5u"):
+            X = torch.randn(32768, 7168, device=dev).bfloat16()
+            ids = torch.arange(32768, device=dev) % 256
+            secondary["c5_uniform"] = gemm_entry(
+                "grouped_gemm bf16 R=32768 H=7168 I=2048 E=256 uniform (arange % 256, 128 rows per expert)",
+                X, W, ids, 1)
+        if want("ep"):
+            X = torch.randn(4096, 7168, device=dev).bfloat16()
+            ids = torch.arange(4096, device=dev) % 32
+            secondary["ep_shard"] = gemm_entry(
+                "grouped_gemm bf16 expert-parallel shard: E_local=32 of 256, R=4096 (128 per expert), H=7168 I=2048",
+                X, W[:32], ids, 1)
+        del W
 
     # ---------------- fused router GEMM + TopK + softmax ----------------
     # The reference's router-fusion benchmark models (benchmarks/benchmark_router_fusion.py:169-174)

@@ -172,6 +172,19 @@ int moe_grouped_gemm(const void* X, const void* W, const void* expert_ids,
                      int64_t I, int64_t E, void* Y, void* workspace,
                      size_t ws_bytes, void* stream);
 
+/* The grouped GEMM of moe_grouped_gemm without its routing sort: it runs on
+ * the routing tables that the previous moe_grouped_gemm call on the same
+ * workspace built, which must have had the same expert_ids, T, topk, I and E
+ * (with nothing else using the workspace since).  The reference's
+ * benchmark does its routing once outside the timed region
+ * (benchmarks/benchmark_grouped_gemm.py:116-130, argsort + bincount); this
+ * is that split on the device, for callers that apply several weight sets
+ * to one routing and for GEMM-only timing.  Arguments as moe_grouped_gemm.
+ */
+int moe_grouped_gemm_routed(const void* X, const void* W, int dtype, int64_t T,
+                            int64_t topk, int64_t H, int64_t I, int64_t E, void* Y,
+                            void* workspace, size_t ws_bytes, void* stream);
+
 /* ---------------------------------------------------------------------
  * Router GEMM (logits = X . W) and the fused router GEMM + TopK + softmax.
  * The weights are used transposed, Wt [E, H], so that both MFMA operands

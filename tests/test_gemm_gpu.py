@@ -176,26 +176,77 @@ def test_config4_fusedmoe_test_shape(cuda):
     assert torch.equal(Y, Y1)
 
 
-def test_config5_deepseek_v3_shape(cuda):
-    """T=4096, H=7168, I=2048, E=256, top-8 skewed routing (32768 rows, W 7.5 GB).
-    Checked on every row of 24 experts (the largest, empty-adjacent and random)."""
-    g = torch.Generator().manual_seed(0)
-    bias = 1.5 * torch.randn(256, generator=g)
-    idx = torch.topk(torch.randn(4096, 256, generator=g) + bias, 8).indices.to(cuda)
+def _c5_weights(cuda):
     gc = torch.Generator(device=cuda).manual_seed(0)
-    X = torch.randn(4096, 7168, generator=gc, device=cuda).bfloat16()
     W = torch.empty(256, 2048, 7168, dtype=torch.bfloat16, device=cuda)
     for e in range(0, 256, 32):
         W[e:e + 32] = (0.02 * torch.randn(32, 2048, 7168, generator=gc, device=cuda)).bfloat16()
+    return W, gc
+
+
+def _check_every_expert(Y, X, W, flat, x_row):
+    """Compares every row of every non-empty expert with an fp32 matmul of
+    that expert (x_row maps routed rows to X rows)."""
+    counts = torch.bincount(flat, minlength=W.shape[0])
+    checked = 0
+    for e in torch.nonzero(counts).squeeze(1).tolist():
+        rows = torch.nonzero(flat == e).squeeze(1)
+        ref = X[x_row(rows)].float() @ W[e].float().T
+        torch.testing.assert_close(Y[rows].float(), ref, rtol=RTOL, atol=ATOL)
+        checked += rows.numel()
+    assert checked == flat.numel()
+
+
+def test_config5_deepseek_v3_shape(cuda):
+    """T=4096, H=7168, I=2048, E=256, top-8 skewed routing (32768 rows, W 7.5 GB).
+    Every row of every one of the 167 non-empty experts is checked."""
+    g = torch.Generator().manual_seed(0)
+    bias = 1.5 * torch.randn(256, generator=g)
+    idx = torch.topk(torch.randn(4096, 256, generator=g) + bias, 8).indices.to(cuda)
+    W, gc = _c5_weights(cuda)
+    X = torch.randn(4096, 7168, generator=gc, device=cuda).bfloat16()
     Y = K.grouped_gemm(X, W, idx)
     torch.cuda.synchronize()
     flat = idx.flatten()
-    counts = torch.bincount(flat, minlength=256)
-    experts = torch.argsort(counts, descending=True)[:8].tolist() + list(range(0, 256, 16))
-    for e in experts:
-        rows = torch.nonzero(flat == e).squeeze(1)
-        if rows.numel() == 0:
-            continue
-        ref = X[rows // 8].float() @ W[e].float().T
-        torch.testing.assert_close(Y[rows].float(), ref, rtol=RTOL, atol=ATOL)
+    assert int((torch.bincount(flat, minlength=256) > 0).sum()) == 167
+    _check_every_expert(Y, X, W, flat, lambda rows: rows // 8)
     del W
+
+
+def test_config5_uniform_routing(cuda):
+    """The C5 shape under the reference benchmark's uniform routing
+    (benchmarks/benchmark_grouped_gemm.py:104-109): 4096 * 8 / 256 = 128 rows
+    per expert, expert_indices = arange(32768) % 256 over an X of 32768 rows
+    (1-D ids, no gather), and its single-GPU expert-parallel shard
+    (E_local = 32 experts, 4096 rows)."""
+    W, gc = _c5_weights(cuda)
+    R = 32768
+    X = torch.randn(R, 7168, generator=gc, device=cuda).bfloat16()
+    ids = torch.arange(R, device=cuda) % 256
+    Y = K.grouped_gemm(X, W, ids)
+    torch.cuda.synchronize()
+    _check_every_expert(Y, X, W, ids, lambda rows: rows)
+    # expert-parallel shard: the first 32 experts, 128 rows each
+    Xs = X[:4096].contiguous()
+    ids_s = torch.arange(4096, device=cuda) % 32
+    Ws = W[:32]
+    Ys = K.grouped_gemm(Xs, Ws, ids_s)
+    torch.cuda.synchronize()
+    _check_every_expert(Ys, Xs, Ws, ids_s, lambda rows: rows)
+    del W
+
+
+def test_reuse_routing_matches_full_call(cuda):
+    """moe_grouped_gemm_routed on the routing tables of the previous call is
+    bitwise the full call, for every tile configuration, with a different
+    weight set on the same routing."""
+    for T, topk, E, H, I in ((300, 2, 8, 256, 96), (4096, 2, 8, 1024, 256), (8192, 4, 64, 512, 512)):
+        X, W = make(T, H, I, E, seed=T)
+        W2 = (0.5 * W).contiguous()
+        g = torch.Generator().manual_seed(T)
+        ids = torch.randint(0, E + 1, (T, topk), generator=g).to(cuda)  # includes invalid ids
+        Y = K.grouped_gemm(X, W, ids)
+        Yr = K.grouped_gemm_reuse_routing(X, W, topk)
+        assert torch.equal(Y, Yr)
+        Y2 = K.grouped_gemm(X, W2, ids)
+        assert torch.equal(K.grouped_gemm_reuse_routing(X, W2, topk), Y2)

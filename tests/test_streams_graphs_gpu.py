@@ -114,29 +114,27 @@ def test_graph_replays_match_eager(cuda):
 
 
 def test_capture_as_first_call_on_a_fresh_stream(cuda):
-    """Workspaces are never allocated inside a capture (they would belong to
-    the graph's private pool): a call that needs one raises with the warm-up
-    hint when it is the first call on the capturing stream, while calls that
-    need none capture and replay correctly as a fresh stream's first call."""
+    """A graph captured with no warm-up on its capture stream (torch's own
+    capture stream, as in torch.cuda.graph(g) after a warm-up elsewhere):
+    the call that needs a workspace makes it inside the capture (graph-pool
+    memory, zero fill recorded in the graph), and every replay matches eager,
+    with eager calls of the same shape between replays."""
     g = torch.Generator(device="cuda").manual_seed(5)
     split = torch.randn(4, 65536, generator=g, device="cuda")   # split rows: needs a workspace
     small = torch.randn(256, 64, generator=g, device="cuda").bfloat16()
-    s = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
-    with pytest.raises(RuntimeError, match="warm-up"):
-        with torch.cuda.graph(graph, stream=s):
-            K.topk_softmax(split, 512)
-    torch.cuda.synchronize()
-    s2 = torch.cuda.Stream()
-    graph2 = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph2, stream=s2):
-        static_out = K.topk_softmax(small, 6)
+    with torch.cuda.graph(graph):
+        static_out = list(K.topk_softmax(split, 512)) + list(K.topk_softmax(small, 6))
+        static_out += list(K.topk_softmax(split, 512))  # a second captured call on the same buffer
     for rep in range(3):
+        split.copy_(torch.randn(4, 65536, generator=g, device="cuda"))
         small.copy_(torch.randn(256, 64, generator=g, device="cuda").bfloat16())
         torch.cuda.synchronize()
-        graph2.replay()
+        graph.replay()
         torch.cuda.synchronize()
-        _assert_equal(static_out, K.topk_softmax(small, 6), f"fresh-stream capture, replay {rep}")
+        want = list(K.topk_softmax(split, 512)) + list(K.topk_softmax(small, 6)) + list(K.topk_softmax(split, 512))
+        torch.cuda.synchronize()
+        _assert_equal(static_out, want, f"first-call capture, replay {rep}")
 
 
 def test_graph_replay_after_workspace_growth(cuda):

@@ -40,6 +40,8 @@ SIGNATURES = {
                                 _c_size, _c_ptr]),
     "moe_grouped_gemm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_i64, _c_i64, _c_i64,
                                   _c_i64, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "moe_grouped_gemm_routed": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                         _c_ptr, _c_ptr, _c_size, _c_ptr]),
     "moe_grouped_gemm_swiglu": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_i64, _c_i64,
                                          _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
     "moe_combine": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
@@ -113,7 +115,8 @@ def current_stream(dev) -> int:
     return torch.cuda.current_stream(idx).cuda_stream
 
 
-_ws_cache = {}    # (device index, raw stream handle) -> (tensor, data_ptr, bytes)
+_ws_cache = {}    # (device index, raw stream handle) -> (tensor, data_ptr, bytes), made outside capture
+_ws_capture = {}  # the same key -> buffer made during a graph capture (graph-pool memory)
 _ws_retired = []  # replaced buffers: a captured graph may still reference them
 _ws_lock = threading.Lock()
 
@@ -126,15 +129,17 @@ def workspace_ptr(dev_index: int, stream: int, nbytes: int) -> int:
     different streams get different buffers.  Every call leaves the
     buffer's control block zero, so a buffer stays valid for the next call
     on its stream, also when torch hands a stream handle to a new stream
-    (its streams live in pools and are never destroyed).
+    (its streams live in pools and are never destroyed).  A buffer that is
+    outgrown is replaced but kept alive: a graph captured earlier may still
+    use it.
 
-    Buffers are made only outside graph capture: one allocated during
-    capture would belong to the graph's private memory pool.  A buffer that
-    is outgrown is replaced but kept alive (a graph captured earlier may
-    still use it).  Inside a capture the stream's existing buffer is used if
-    it is large enough; otherwise this raises, and the caller must make one
-    eager call of the same or a larger size on that stream before capture
-    (the usual warm-up)."""
+    Inside a graph capture the stream's buffer is used if it is large
+    enough.  Otherwise a buffer is made in the capture (it comes from the
+    graph's memory pool, and its zero fill is recorded in the graph, so it
+    is zero at the start of every replay); such a buffer serves later
+    captured calls on that stream, is never used by eager calls, and is kept
+    alive for the life of the process.  Graphs that share a buffer must not
+    be replayed concurrently."""
     if nbytes == 0:
         return 0
     ent = _ws_cache.get((dev_index, stream))
@@ -147,22 +152,20 @@ def _grow(dev_index: int, stream: int, nbytes: int):
     import torch
 
     key = (dev_index, stream)
+    capturing = torch.cuda.is_current_stream_capturing()
+    cache = _ws_capture if capturing else _ws_cache
     with _ws_lock:
-        ent = _ws_cache.get(key)
+        ent = cache.get(key)
         if ent is not None and ent[2] >= nbytes:
             return ent
-        if torch.cuda.is_current_stream_capturing():
-            have = 0 if ent is None else ent[2]
-            raise RuntimeError(
-                f"tilelang_moe_amd: this call needs a {nbytes}-byte device workspace on the capturing stream, "
-                f"which has {have} bytes; workspaces are not allocated during graph capture. Run the same "
-                "call once eagerly on this stream before capturing (warm-up).")
         size = max(nbytes, 1 << 16, 2 * (ent[2] if ent is not None else 0))
         buf = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", dev_index))
         if ent is not None:
             _ws_retired.append(ent[0])
         ent = (buf, buf.data_ptr(), size)
-        _ws_cache[key] = ent
+        cache[key] = ent
+        if capturing:
+            _ws_retired.append(buf)  # graph-pool memory: never released by this package
         return ent
 
 

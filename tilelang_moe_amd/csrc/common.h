@@ -69,7 +69,8 @@ int router_gemm_logits_or_partials(const void* X, const void* Wt, int dtype, int
 // T*topk .. T*topk + Tx - 1 form expert E, with weights Wx (and W2x for the
 // SwiGLU epilogue) and X row r - T*topk + x_shift.  reuse_bm = 0 sorts the
 // rows; reuse_bm = b > 0 reuses the routing tables an earlier call on the
-// same workspace built for the same rows with tile height b (bm_used).
+// same workspace built for the same rows with tile height b (bm_used);
+// reuse_bm < 0 reuses the tables of an earlier call of the same shape.
 struct GemmExtra {
   const void* Wx = nullptr;
   const void* W2x = nullptr;
@@ -89,29 +90,6 @@ constexpr int kWave = 64;
 // entry point in turn on one stream.
 constexpr size_t kWsCtlBytes = 4096;
 
-// Phase timestamps for kernel tuning builds (-DMOE_PHASE_TIMING, which
-// also provides moe_phase[] and moe_phase_lds[]): thread 0 of each
-// workgroup records the wall clock of phase `slot` in LDS, and
-// MOE_PHASE_FLUSH() copies the record to moe_phase[block][slot] once, so
-// the timestamps add no global stores (which barriers would wait for)
-// inside the timed phases.
-#ifdef MOE_PHASE_TIMING
-#define MOE_PHASE(slot)                                              \
-  do {                                                               \
-    if (threadIdx.x == 0) moe_phase_lds[(slot)] = wall_clock64();    \
-  } while (0)
-#define MOE_PHASE_FLUSH()                                            \
-  do {                                                               \
-    if (threadIdx.x < 32) moe_phase[blockIdx.x * 32 + threadIdx.x] = moe_phase_lds[threadIdx.x]; \
-  } while (0)
-#else
-#define MOE_PHASE(slot) \
-  do {                  \
-  } while (0)
-#define MOE_PHASE_FLUSH() \
-  do {                    \
-  } while (0)
-#endif
 
 // Workgroup barrier that orders LDS only.  __syncthreads() carries a
 // workgroup fence over every address space, which waits for all of the

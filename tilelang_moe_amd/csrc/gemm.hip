@@ -671,7 +671,7 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
     return fail(MOE_EINVAL, f + ": X, W and Y must be bfloat16 or float16");
   if (idx_dtype != MOE_I32 && idx_dtype != MOE_I64) return fail(MOE_EINVAL, f + ": expert ids must be int32 or int64");
   if (R == 0) return MOE_OK;
-  if (!X || !W || (R_ids > 0 && !expert_ids) || !Y || (EPI == 1 && !W2) ||
+  if (!X || !W || (R_ids > 0 && !expert_ids && ex.reuse_bm == 0) || !Y || (EPI == 1 && !W2) ||
       (ex.Tx > 0 && (!ex.Wx || (EPI == 1 && !ex.W2x))))
     return fail(MOE_EINVAL, f + ": null pointer");
   if (((uintptr_t)X | (uintptr_t)W | (uintptr_t)W2 | (uintptr_t)ex.Wx | (uintptr_t)ex.W2x) & 15)
@@ -705,7 +705,7 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
     else
       rc = launch_route(static_cast<const int32_t*>(expert_ids), R, R_ids, (int)E, (int)Et, blockcnt, counts, offsets,
                         sorted, bm, t_exp, t_ms, meta, st);
-  } else if (ex.reuse_bm != bm) {
+  } else if (ex.reuse_bm > 0 && ex.reuse_bm != bm) {  // reuse_bm < 0: the tables were built for this shape
     route_tiles_kernel<<<1, kScanThreads, 0, st>>>(offsets, (int)Et, bm, t_exp, t_ms, meta);
     rc = check_launch("route_tiles_kernel");
   }
@@ -755,4 +755,13 @@ extern "C" int moe_grouped_gemm_swiglu(const void* X, const void* Wg, const void
                                        void* stream) {
   return grouped_gemm_impl<1>("grouped_gemm_swiglu", X, Wg, Wu, expert_ids, dtype, idx_dtype, T, topk, H, I, E,
                               GemmExtra{}, Y, workspace, ws_bytes, stream, nullptr);
+}
+
+extern "C" int moe_grouped_gemm_routed(const void* X, const void* W, int dtype, int64_t T, int64_t topk, int64_t H,
+                                       int64_t I, int64_t E, void* Y, void* workspace, size_t ws_bytes,
+                                       void* stream) {
+  GemmExtra ex;
+  ex.reuse_bm = -1;  // the routing tables of the previous call of this shape on this workspace
+  return grouped_gemm_impl<0>("grouped_gemm_routed", X, W, nullptr, nullptr, dtype, MOE_I32, T, topk, H, I, E, ex, Y,
+                              workspace, ws_bytes, stream, nullptr);
 }

@@ -578,13 +578,10 @@ __device__ inline uint32_t sample_bound(uint32_t samp, int K, int N, uint32_t* h
   const int tid = threadIdx.x;
   for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
   lds_barrier();
-  MOE_PHASE(16);
   wave_aggregated_add(hist, samp >> 21, true, 11);
   lds_barrier();
-  MOE_PHASE(17);
   RadixState ss{0u, 0u, (uint32_t)m_rank, 0u, false};
   radix_pick_bin_w0(ss, hist, 21, 0x7FFu, s_pick);
-  MOE_PHASE(18);
   // Samples at or above the bin's lower edge estimate the candidate count.
   const uint32_t at_or_above = (uint32_t)m_rank - ss.need + ss.eq_count;
   if (!ss.all_taken && (float)at_or_above * ((float)N / kSample) > 0.5f * kCandCap) {
@@ -652,14 +649,12 @@ __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t
     in[u] = p < C;
     v[u] = in[u] ? cand[p] : 0ull;
   }
-  MOE_PHASE(8);
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     bk[u] = bucket(v[u]);
     if (in[u]) atomicAdd(&hist[bk[u]], 1u);
   }
   __syncthreads();
-  MOE_PHASE(9);
   {
     uint32_t h[BPT], hs = 0, hmax = 0;
 #pragma unroll
@@ -682,7 +677,6 @@ __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t
     if (lane == 0 && hmax > (uint32_t)kBucketFixMax) *s_flag = 1;
   }
   __syncthreads();
-  MOE_PHASE(10);
   if (*s_flag) {
     // Crowded bucket: sort all candidates instead (cand[] is intact).
     const int Cpad = next_pow2_dev(C);
@@ -699,7 +693,6 @@ __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t
   for (int u = 0; u < U; ++u)
     if (in[u] && (int)bstart[bk[u]] < K) tmp[atomicAdd(&hist[bk[u]], 1u)] = v[u];
   __syncthreads();
-  MOE_PHASE(11);
   // Rank = bucket start + larger composites in the bucket (buckets hold at
   // most kBucketFixMax candidates).  Thread t now ranks the candidates at
   // sorted positions t + 1024 u < Cw, so the lanes of a wave share buckets.
@@ -732,7 +725,6 @@ __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t
 #pragma unroll
       for (int q = 0; q < 4; ++q) rk[u] += (j + q < len[u]) & (t[u][q] > v[u]);
   }
-  MOE_PHASE(12);
   // The normaliser is summed exactly, in fixed point, so the scores are
   // bitwise reproducible whatever (atomic) order the candidates reached
   // threads in: every winner's exp lies in [0, 1] and is converted to
@@ -756,7 +748,6 @@ __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t
   qsum = wave_sum_u64(qsum);
   if (lane == 0) s_sum64[tid / kWave] = __ballot(nan) ? ~0ull : qsum;
   __syncthreads();
-  MOE_PHASE(13);
   uint64_t total = 0;
   bool any_nan = false;
 #pragma unroll
@@ -770,7 +761,6 @@ __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t
     const uint64_t e = cand[r];
     store_out(scores, indices, row * K + r, __uint_as_float((uint32_t)(e >> 32)) / sum, (uint32_t)e);
   }
-  MOE_PHASE(14);
 }
 
 template <typename IdxT>
@@ -962,7 +952,6 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   const int64_t row = blockIdx.x;
   const T* x = logits + row * ld;
 
-  MOE_PHASE(0);
   // The sample load goes first so that the bound waits for it alone while
   // the row loads are still in flight.
   const uint32_t samp = sample_key(x, N);
@@ -970,7 +959,6 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   issue_row_loads<T, VEC, KPT>(x, 0, N, key);
   if (tid == 0) s_max = 0;
   const uint32_t L = sample_bound(samp, K, N, hist, s_pick);  // has barriers
-  MOE_PHASE(1);
   bool special = false;
   keys_from_bits<T, VEC, KPT>(x, 0, N, key, special);
   rekey_if_special<KPT>(key, special);
@@ -979,7 +967,6 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   for (int i = 0; i < KPT; ++i) kmax = max(kmax, key[i]);
   kmax = wave_max_u32(kmax);
   if (lane == 0) atomicMax(&s_max, kmax);
-  MOE_PHASE(2);
 
   // ---- candidate mask: keys >= L, else exact mode ----
   uint32_t mask = 0;
@@ -1050,7 +1037,6 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
     cpos = block_excl_scan_1024((uint32_t)__popc(mask), wsum, &C);  // C == K
     base = st.prefix;
   }
-  MOE_PHASE(3);
   const uint32_t rmax = s_max;  // complete: the scans above hold barriers
 
   // ---- extraction from the key registers (fully unrolled, no indexing) ----
@@ -1059,11 +1045,8 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
     if ((mask >> i) & 1u) cand[cpos++] = make_comp(key[i], slot_col<VEC>(0, i));
   order_prepare(hist, s_flag);
   __syncthreads();
-  MOE_PHASE(4);
   order_and_store(cand, (int)C, base, rmax, K, row, tmp, hist, bstart, wsum, s_flag, s_red, scores, indices,
                   s_sum64);
-  MOE_PHASE(5);
-  MOE_PHASE_FLUSH();
 }
 
 // ===========================================================================
@@ -1119,13 +1102,11 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   const int c0 = g * slice;
   const int end = min(N, c0 + slice);
 
-  MOE_PHASE(0);
   const uint32_t samp = sample_key(x, N);
   uint32_t key[KPT];
   issue_row_loads<T, VEC, KPT>(x, c0, end, key);
   if (tid == 0) s_max = 0;
   const uint32_t L = sample_bound(samp, K, N, hist, s_pick);  // has barriers
-  MOE_PHASE(1);
   bool special = false;
   keys_from_bits<T, VEC, KPT>(x, c0, end, key, special);
   rekey_if_special<KPT>(key, special);
@@ -1134,7 +1115,6 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   for (int i = 0; i < KPT; ++i) kmax = max(kmax, key[i]);
   kmax = wave_max_u32(kmax);
   if (lane == 0) atomicMax(&s_max, kmax);
-  MOE_PHASE(2);
 
   uint32_t mask = 0;
 #pragma unroll
@@ -1147,7 +1127,6 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   }
   __syncthreads();
   cpos += s_base;
-  MOE_PHASE(3);
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
     if ((mask >> i) & 1u) {
@@ -1157,7 +1136,6 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
       ++cpos;
     }
   }
-  MOE_PHASE(4);
   // Publish, then count in.  The candidates went out as agent-scope atomic
   // stores, which write through the XCD's L2, so waiting for this
   // workgroup's stores to complete is the whole release: no L2 writeback
@@ -1167,7 +1145,6 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   __syncthreads();
   if (tid == 0) s_last = __hip_atomic_fetch_add(&rc->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(G - 1);
   __syncthreads();
-  MOE_PHASE(5);
   if (!s_last) return;
 
   // ---- last workgroup of the row ----
@@ -1189,11 +1166,8 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
     cand[p] = __hip_atomic_load(rcand + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   order_prepare(hist, s_flag);
   __syncthreads();
-  MOE_PHASE(6);
   order_and_store(cand, (int)C, L, rmax, K, row, tmp, hist, bstart, wsum, s_flag, s_red, scores, indices,
                   s_sum64);
-  MOE_PHASE(7);
-  MOE_PHASE_FLUSH();
 }
 
 // ===========================================================================
@@ -1448,9 +1422,6 @@ static int num_cus() {
 constexpr int64_t kSplitMaxRows = kWsCtlBytes / sizeof(SplitRowCtl);
 constexpr int kSplitMaxG = 64;
 
-#ifdef MOE_PHASE_TIMING
-int moe_split_g_override = 0;  // tuning builds only
-#endif
 
 // Rows too long for one workgroup's registers are split over G workgroups
 // (G a power of two, slice <= 1024 * kRadixRegMaxKPT keys).  Rows that fit
@@ -1460,9 +1431,6 @@ int moe_split_g_override = 0;  // tuning builds only
 // workgroup takes 128 KB of LDS).
 static int split_groups(int64_t M, int64_t N, int64_t K) {
   if (K > kRadixRegMaxK || M < 1 || M > kSplitMaxRows) return 1;
-#ifdef MOE_PHASE_TIMING
-  if (moe_split_g_override) return moe_split_g_override;
-#endif
   const int64_t cap = (int64_t)kRadixThreads * kRadixRegMaxKPT;
   if (N <= cap) return 1;
   int G = 1;

@@ -25,7 +25,7 @@ from .topk_softmax import (
     topk_softmax_separate,
     topk_softmax_sonic,
 )
-from .grouped_gemm import grouped_gemm, grouped_gemm_best, route_sort
+from .grouped_gemm import grouped_gemm, grouped_gemm_best, grouped_gemm_reuse_routing, route_sort
 from .fusedmoe import (
     FusedMoETileLang,
     FusedMoETileLangStreams,
@@ -64,6 +64,7 @@ __all__ = [
     "select_strategy",
     "grouped_gemm",
     "grouped_gemm_best",
+    "grouped_gemm_reuse_routing",
     "route_sort",
     "router_gemm",
     "router_topk_softmax",
