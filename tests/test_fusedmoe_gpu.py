@@ -170,3 +170,20 @@ def test_reference_signatures(cuda):
     assert torch.equal(m.forward(*args), out)
     flat = K.fused_moe_routed(x, **w, n_experts_per_token=k)
     assert torch.equal(flat.view(B, S, Dh), out)
+
+
+def test_grouped_gemm_swiglu_mixed_tile_heights(cuda):
+    """SwiGLU epilogue on a problem that takes the tallest tiles, with
+    skewed routing so that small experts get short tiles."""
+    T, topk, E, H, I = 4096, 8, 64, 512, 512
+    g = torch.Generator().manual_seed(41)
+    bias = 1.5 * torch.randn(E, generator=g)
+    ids = torch.topk(torch.randn(T, E, generator=g) + bias, topk).indices.to(cuda)
+    counts = torch.bincount(ids.flatten(), minlength=E)
+    assert (counts > 256).any() and ((counts > 0) & (counts <= 128)).any()
+    gd = torch.Generator(device="cuda").manual_seed(41)
+    X = rnd(T, H, g=gd, scale=1.0)
+    Wg, Wu = rnd(E, I, H, g=gd), rnd(E, I, H, g=gd)
+    Y = K.grouped_gemm_swiglu(X, Wg, Wu, ids)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(Y.float(), swiglu_ref(X, Wg, Wu, ids, topk), rtol=1e-2, atol=1e-2)

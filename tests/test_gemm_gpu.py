@@ -250,3 +250,32 @@ def test_reuse_routing_matches_full_call(cuda):
         assert torch.equal(Y, Yr)
         Y2 = K.grouped_gemm(X, W2, ids)
         assert torch.equal(K.grouped_gemm_reuse_routing(X, W2, topk), Y2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mixed_tile_heights(cuda, dtype):
+    """Problems that take the tallest tiles mix them with short tiles: an
+    expert of at most 128 rows gets one short tile (three-stage pipeline),
+    larger ones tiles of 256 rows.  Skewed routing with experts of every
+    size class, including exactly 128 and 129 rows, and invalid ids."""
+    T, topk, E, H, I = 4096, 8, 96, 256, 1024
+    g = torch.Generator().manual_seed(31)
+    bias = 1.5 * torch.randn(E, generator=g)
+    ids = torch.topk(torch.randn(T, E, generator=g) + bias, topk).indices
+    flat = ids.flatten()
+    flat[::211] = E + 7  # invalid
+    # Force two experts to exactly 128 and 129 rows by re-routing rows of the largest expert.
+    big = int(torch.bincount(flat[flat < E], minlength=E).argmax())
+    for e, want in ((E - 1, 128), (E - 2, 129)):
+        have = int((flat == e).sum())
+        if have < want:
+            src = torch.nonzero(flat == big).squeeze(1)[: want - have]
+            flat[src] = e
+        else:
+            flat[torch.nonzero(flat == e).squeeze(1)[: have - want]] = big
+    ids = flat.view(T, topk)
+    counts = torch.bincount(flat[flat < E], minlength=E)
+    assert int(counts[E - 1]) == 128 and int(counts[E - 2]) == 129
+    assert (counts > 256).any() and ((counts > 0) & (counts <= 128)).any()
+    X, W = make(T, H, I, E, seed=31, dtype=dtype)
+    check_gemm(X, W, ids.to(cuda), topk)

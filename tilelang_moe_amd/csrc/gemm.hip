@@ -21,12 +21,19 @@
 
 #include <algorithm>
 #include <string>
+#include <type_traits>
 
 namespace moe {
 
 constexpr int kRouteThreads = 256;
 constexpr int kMaxExperts = 4096;
 constexpr int kScanThreads = 1024;
+// Tile tables may mix two tile heights: an entry of tile_expert with this
+// bit set is a short tile (the second configuration of the GEMM kernel).
+// The tile height argument `bm` of the routing kernels is then
+// tall | short << 12: experts with at most `short` rows get one short tile,
+// the others tiles of `tall` rows.
+constexpr int32_t kShortTile = 1 << 30;
 
 // Bucket of routed row r.  Rows r < R_ids carry an expert id, valid in
 // [0, E_ids); rows r >= R_ids (an appended set, e.g. a shared expert taken
@@ -133,19 +140,30 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
 
 // The M-tile table for tile height bm from segment offsets already in LDS
 // (s_off[0..E], published by a barrier): expert e owns ceil(count_e / bm)
-// consecutive M tiles; meta[0] = number of tiles.  One block (any size).
+// consecutive M tiles, or one short tile when bm = tall | short << 12 and
+// count_e <= short; meta[0] = number of tiles.  One block (any size).
 __device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int32_t* wsum,
                                         int32_t* __restrict__ tile_expert, int32_t* __restrict__ tile_mstart,
                                         int32_t* __restrict__ meta) {
   const int tid = threadIdx.x;
+  const int tall = bm & 0xFFF, shrt = bm >> 12;
   const int perE = (E + (int)blockDim.x - 1) / (int)blockDim.x;
   const int elo = std::min(E, tid * perE), ehi = std::min(E, elo + perE);
   int32_t nt = 0;
-  for (int e = elo; e < ehi; ++e) nt += (s_off[e + 1] - s_off[e] + bm - 1) / bm;
+  for (int e = elo; e < ehi; ++e) {
+    const int32_t c = s_off[e + 1] - s_off[e];
+    nt += (c > 0 && c <= shrt) ? 1 : (c + tall - 1) / tall;
+  }
   int32_t t = block_excl_scan(nt, wsum);
   for (int e = elo; e < ehi; ++e) {
     const int32_t c = s_off[e + 1] - s_off[e];
-    for (int32_t m = 0; m < c; m += bm, ++t) {
+    if (c > 0 && c <= shrt) {
+      tile_expert[t] = e | kShortTile;
+      tile_mstart[t] = s_off[e];
+      ++t;
+      continue;
+    }
+    for (int32_t m = 0; m < c; m += tall, ++t) {
       tile_expert[t] = e;
       tile_mstart[t] = s_off[e] + m;
     }
@@ -341,90 +359,27 @@ constexpr int kMinBM = 64;  // smallest M tile of any configuration (workspace s
 using CfgHuge = GemmCfg<256, 256, 2, 4, 64, 2, 1>;   // 8 waves of 128x64, 128 KB LDS, 1 per CU
 using CfgLarge = GemmCfg<128, 256, 2, 2, 32, 2, 2>;  // 4 waves of 64x128,  48 KB LDS, 2 per CU
 using CfgSmall = GemmCfg<64, 128, 2, 2, 64, 3, 2>;   // 4 waves of 32x64,   72 KB LDS, 2 per CU
+using CfgShort = GemmCfg<128, 256, 2, 4, 64, 3, 1>;  // 8 waves of 64x64, 144 KB LDS: short tiles beside CfgHuge
+template <typename C> struct TypeC { using type = C; };
 
+// One output tile: rows m0 .. min(m0 + BM, mend) of expert e's segment,
+// output columns n0 .. n0 + OBN.
 // EPI 0: Y = X W^T.  EPI 1 (SwiGLU): Y = silu(X Wg^T) * (X Wu^T) with W = Wg and
 // W2 = Wu, both [E, I, H]; a tile then covers BN/2 output columns, its even
 // 32-column blocks holding gate rows and its odd blocks the up rows of the
 // same output columns, so a lane holds both factors of each output element.
-template <typename T, typename Cfg, int MODE = 0, int EPI = 0>  // MODE: tuning builds only (1 = copies only, 2 = MFMA only)
-__global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
-    const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
-    const uint16_t* __restrict__ Wx, const uint16_t* __restrict__ W2x, uint16_t* __restrict__ Y,
-    int64_t H, int64_t I, int topk, int64_t R, int E, int ntn, int64_t R_ids, int E_ids, int64_t x_shift,
-    const int32_t* __restrict__ sorted_rows, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_mstart,
-    const int32_t* __restrict__ meta) {
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, CPR = Cfg::CPR;
-  constexpr int OBN = EPI == 1 ? BN / 2 : BN;  // output columns per tile
+template <typename T, typename Cfg, int MODE, int EPI>
+__device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* __restrict__ X,
+                                 const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
+                                 const uint16_t* __restrict__ Wx, const uint16_t* __restrict__ W2x,
+                                 uint16_t* __restrict__ Y, int64_t H, int64_t I, int topk, int64_t R_ids, int E_ids,
+                                 int64_t x_shift, const int32_t* __restrict__ sorted_rows, int e, int m0, int mend,
+                                 int n0) {
+  constexpr int BM = Cfg::BM;
   static_assert(EPI == 0 || Cfg::FN % 2 == 0, "SwiGLU pairs 32-column blocks within a wave");
-  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];  // [S][(BM+BN)*BK]
-  __shared__ __attribute__((aligned(16))) int32_t srow[BM];
-
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-
-  // Work list and its order.  The grid is persistent: gridDim.x = 8 * SUPER
-  // workgroups, SUPER per XCD (the hardware deals consecutive workgroups
-  // round-robin over the 8 XCDs, so workgroup b runs on XCD b % 8).  Work is
-  // cut into super-tiles of SUPER items, SM M tiles x SN N tiles; in round i
-  // XCD x processes super-tile 8i + x, one item per workgroup.  The SN N
-  // tiles of an M tile share its gathered X rows and the SM M tiles of one
-  // expert share its weight slices in that XCD's L2, at the same K position,
-  // so a hot expert's weights are read from HBM about ceil(M_e / (SM*BM))
-  // times instead of once per M tile.  The tiles that zero rows whose
-  // expert id lies outside [0, E) follow the super-tiles.
-  constexpr int SUPER = Cfg::SUPER;
-  const int SN = min(ntn, Cfg::SN_MAX);
-  const int SM = SUPER / SN;
-  const int NG = (ntn + SN - 1) / SN;
-  const int n_tiles = meta[0];
-  const int n_super_raw = (n_tiles + SM - 1) / SM * NG * SUPER;
-  // Super-tile order needs the persistent grid and enough super-tiles to
-  // keep every XCD busy for a few rounds.
-  const bool by_super_raw = gridDim.x == 8 * SUPER && n_super_raw / SUPER >= 16;
-  // Length of the tile part of the list: padded to whole super-tiles when
-  // ordered by super-tile, exact otherwise.
-  const int n_super_items = by_super_raw ? n_super_raw : n_tiles * ntn;
-  const int64_t n_bad = R - offsets[E];
-  const int n_zero = (int)((n_bad + BM - 1) / BM) * ntn;
-  const int total = n_super_items + n_zero;
-  // Otherwise (small problems) each XCD takes one contiguous eighth of the
-  // list, its gridDim.x / 8 workgroups walking it in strides.
-  const bool by_super = by_super_raw;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int share = (total + 7) >> 3;
-  int w = by_super ? xcd * SUPER + slot : xcd * share + slot;
-  const int w_end = by_super ? total : min(total, (xcd + 1) * share);
-  const int step = by_super ? (int)gridDim.x : (int)(gridDim.x >> 3);
-  for (; w < w_end; w += step) {
-  __syncthreads();  // the previous tile's LDS reads are done
-  if (w >= n_super_items) {
-    const int z = w - n_super_items;
-    const int64_t z0 = (int64_t)offsets[E] + (int64_t)(z / ntn) * BM;
-    const int n0z = (z % ntn) * OBN;
-    for (int i = tid; i < BM * OBN; i += Cfg::THREADS) {
-      const int64_t p = z0 + i / OBN;
-      const int64_t col = n0z + i % OBN;
-      if (p < R && col < I) Y[(int64_t)sorted_rows[p] * I + col] = 0;
-    }
-    continue;
-  }
-  int mt, nt;
-  if (by_super) {
-    const int sup = w / SUPER, within = w % SUPER;
-    mt = (sup / NG) * SM + within / SN;
-    nt = (sup % NG) * SN + within % SN;
-  } else {
-    mt = w / ntn;  // list order M-major
-    nt = w % ntn;
-  }
-  if (mt >= n_tiles || nt >= ntn) continue;
-  const int n0 = nt * OBN;  // first output column of the tile
-
-  const int e = tile_expert[mt];
-  const int m0 = tile_mstart[mt];
-  const int mend = offsets[e + 1];
   for (int r = tid; r < BM; r += Cfg::THREADS) srow[r] = (m0 + r < mend) ? sorted_rows[m0 + r] : -1;
   // Expert e < E_ids reads W[e] (and W2[e]); the appended expert E_ids reads
   // Wx (and W2x).  X row of routed row r: r / topk for r < R_ids, else
@@ -435,6 +390,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
 
   // Copy plan: instruction i of wave v covers tile rows RPI*(v*INS + i) ..;
   // lane l fills slot l: row l / CPR, position l % CPR.
+  constexpr int CPR = Cfg::CPR;
   const int crow = lane / CPR;
   const int cchunk = (lane % CPR) ^ ((crow / (8 / CPR)) % CPR);
   const uint16_t* a_src[Cfg::A_INS];
@@ -507,6 +463,99 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
       }
     }
   }
+}
+
+// The persistent grouped GEMM over the tile table.  Tiles of Cfg's height,
+// and, when CfgS is not void, short tiles (kShortTile) of CfgS's height:
+// the tile table gives experts with at most CfgS::BM rows one short tile,
+// whose three-stage pipeline keeps twice the weight bytes in flight of the
+// tall tiles' two stages.  Both share the N tiling, the workgroup size and
+// one LDS buffer.
+template <typename T, typename Cfg, typename CfgS, int MODE = 0, int EPI = 0>  // MODE: tuning builds only (1 = copies only, 2 = MFMA only)
+__global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
+    const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
+    const uint16_t* __restrict__ Wx, const uint16_t* __restrict__ W2x, uint16_t* __restrict__ Y,
+    int64_t H, int64_t I, int topk, int64_t R, int E, int ntn, int64_t R_ids, int E_ids, int64_t x_shift,
+    const int32_t* __restrict__ sorted_rows, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_mstart,
+    const int32_t* __restrict__ meta) {
+  constexpr bool MIXED = !std::is_void<CfgS>::value;
+  using CS = typename std::conditional<MIXED, CfgS, Cfg>::type;
+  static_assert(CS::THREADS == Cfg::THREADS && CS::BN == Cfg::BN && CS::MINB == Cfg::MINB,
+                "tile configurations of one kernel share threads, N tiling and occupancy");
+  constexpr int BM = Cfg::BM, BN = Cfg::BN;
+  constexpr int OBN = EPI == 1 ? BN / 2 : BN;  // output columns per tile
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];  // [S][(BM+BN)*BK] of either configuration
+  __shared__ __attribute__((aligned(16))) int32_t srow[BM > CS::BM ? BM : CS::BM];
+
+  const int tid = threadIdx.x;
+
+  // Work list and its order.  The grid is persistent: gridDim.x = 8 * SUPER
+  // workgroups, SUPER per XCD (the hardware deals consecutive workgroups
+  // round-robin over the 8 XCDs, so workgroup b runs on XCD b % 8).  Work is
+  // cut into super-tiles of SUPER items, SM M tiles x SN N tiles; in round i
+  // XCD x processes super-tile 8i + x, one item per workgroup.  The SN N
+  // tiles of an M tile share its gathered X rows and the SM M tiles of one
+  // expert share its weight slices in that XCD's L2, at the same K position,
+  // so a hot expert's weights are read from HBM about ceil(M_e / (SM*BM))
+  // times instead of once per M tile.  The tiles that zero rows whose
+  // expert id lies outside [0, E) follow the super-tiles.
+  constexpr int SUPER = Cfg::SUPER;
+  const int SN = min(ntn, Cfg::SN_MAX);
+  const int SM = SUPER / SN;
+  const int NG = (ntn + SN - 1) / SN;
+  const int n_tiles = meta[0];
+  const int n_super_raw = (n_tiles + SM - 1) / SM * NG * SUPER;
+  // Super-tile order needs the persistent grid and enough super-tiles to
+  // keep every XCD busy for a few rounds.
+  const bool by_super_raw = gridDim.x == 8 * SUPER && n_super_raw / SUPER >= 16;
+  // Length of the tile part of the list: padded to whole super-tiles when
+  // ordered by super-tile, exact otherwise.
+  const int n_super_items = by_super_raw ? n_super_raw : n_tiles * ntn;
+  const int64_t n_bad = R - offsets[E];
+  const int n_zero = (int)((n_bad + BM - 1) / BM) * ntn;
+  const int total = n_super_items + n_zero;
+  // Otherwise (small problems) each XCD takes one contiguous eighth of the
+  // list, its gridDim.x / 8 workgroups walking it in strides.
+  const bool by_super = by_super_raw;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int share = (total + 7) >> 3;
+  int w = by_super ? xcd * SUPER + slot : xcd * share + slot;
+  const int w_end = by_super ? total : min(total, (xcd + 1) * share);
+  const int step = by_super ? (int)gridDim.x : (int)(gridDim.x >> 3);
+  for (; w < w_end; w += step) {
+    __syncthreads();  // the previous tile's LDS reads are done
+    if (w >= n_super_items) {
+      const int z = w - n_super_items;
+      const int64_t z0 = (int64_t)offsets[E] + (int64_t)(z / ntn) * BM;
+      const int n0z = (z % ntn) * OBN;
+      for (int i = tid; i < BM * OBN; i += Cfg::THREADS) {
+        const int64_t p = z0 + i / OBN;
+        const int64_t col = n0z + i % OBN;
+        if (p < R && col < I) Y[(int64_t)sorted_rows[p] * I + col] = 0;
+      }
+      continue;
+    }
+    int mt, nt;
+    if (by_super) {
+      const int sup = w / SUPER, within = w % SUPER;
+      mt = (sup / NG) * SM + within / SN;
+      nt = (sup % NG) * SN + within % SN;
+    } else {
+      mt = w / ntn;  // list order M-major
+      nt = w % ntn;
+    }
+    if (mt >= n_tiles || nt >= ntn) continue;
+    const int te = tile_expert[mt];
+    const int e = te & ~kShortTile;
+    const int m0 = tile_mstart[mt];
+    const int mend = offsets[e + 1];
+    if (MIXED && (te & kShortTile))
+      gemm_tile<T, CS, MODE, EPI>(smem, srow, X, W, W2, Wx, W2x, Y, H, I, topk, R_ids, E_ids, x_shift,
+                                     sorted_rows, e, m0, mend, nt * OBN);
+    else
+      gemm_tile<T, Cfg, MODE, EPI>(smem, srow, X, W, W2, Wx, W2x, Y, H, I, topk, R_ids, E_ids, x_shift,
+                                        sorted_rows, e, m0, mend, nt * OBN);
   }  // tile loop
 }
 
@@ -591,18 +640,20 @@ static int launch_route(const IdxT* ids, int64_t R, int64_t R_ids, int E_ids, in
   return check_launch("route_scatter_kernel");
 }
 
-template <typename T, typename Cfg, int MODE = 0, int EPI = 0>
+template <typename T, typename Cfg, typename CfgS, int MODE = 0, int EPI = 0>
 static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, const uint16_t* w2, const uint16_t* wx,
                        const uint16_t* w2x, uint16_t* y, int64_t H, int64_t I, int topk, int64_t R, int E, int ntn,
                        int64_t R_ids, int E_ids, int64_t x_shift, const int32_t* sorted, const int32_t* offsets,
                        const int32_t* t_exp, const int32_t* t_ms, const int32_t* meta) {
+  using CS = typename std::conditional<std::is_void<CfgS>::value, Cfg, CfgS>::type;
+  constexpr size_t lds = Cfg::LDS_BYTES > CS::LDS_BYTES ? Cfg::LDS_BYTES : CS::LDS_BYTES;
   static std::atomic<uint64_t> lds_cap_set{0};
-  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_kernel<T, Cfg, MODE, EPI>, (int)Cfg::LDS_BYTES, st));
+  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_kernel<T, Cfg, CfgS, MODE, EPI>, (int)lds, st));
   // Persistent grid of SUPER workgroups per XCD (8 XCDs x 32 CUs x MINB) when
   // the tile list can be long; otherwise one workgroup per possible tile.
   const int64_t ub = ((R + Cfg::BM - 1) / Cfg::BM + E + 1) * ntn;  // tiles, upper bound
   const int64_t grid = ub >= 16 * Cfg::SUPER ? 8 * Cfg::SUPER : (ub + 7) / 8 * 8;
-  grouped_gemm_kernel<T, Cfg, MODE, EPI><<<dim3((unsigned)grid), Cfg::THREADS, Cfg::LDS_BYTES, st>>>(
+  grouped_gemm_kernel<T, Cfg, CfgS, MODE, EPI><<<dim3((unsigned)grid), Cfg::THREADS, lds, st>>>(
       x, w, w2, wx, w2x, y, H, I, topk, R, E, ntn, R_ids, E_ids, x_shift, sorted, offsets, t_exp, t_ms, meta);
   return MOE_OK;
 }
@@ -694,7 +745,7 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   // MFMA; smaller problems take smaller tiles to fill the chip.
   auto tiles_of = [&](int64_t bm, int64_t bn) { return ((R + bm - 1) / bm) * ((Iv + bn - 1) / bn); };
   const int cfg = tiles_of(CfgHuge::BM, CfgHuge::BN) >= 512 ? 2 : tiles_of(CfgLarge::BM, CfgLarge::BN) >= 512 ? 1 : 0;
-  const int bm = cfg == 2 ? CfgHuge::BM : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
+  const int bm = cfg == 2 ? CfgHuge::BM | CfgShort::BM << 12 : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
   const int bn = cfg == 2 ? CfgHuge::BN : cfg == 1 ? CfgLarge::BN : CfgSmall::BN;
   if (bm_used) *bm_used = bm;
   int rc = MOE_OK;
@@ -718,15 +769,17 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   const uint16_t* wx = static_cast<const uint16_t*>(ex.Wx);
   const uint16_t* w2x = static_cast<const uint16_t*>(ex.W2x);
   uint16_t* y = static_cast<uint16_t*>(Y);
-  auto run = [&](auto cfg_tag) {
+  auto run = [&](auto cfg_tag, auto cfgs_tag) {
     using C = decltype(cfg_tag);
+    using CS = typename decltype(cfgs_tag)::type;
     return dtype == MOE_BF16
-               ? launch_gemm<uint16_t, C, 0, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn, R_ids,
-                                                 (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta)
-               : launch_gemm<Half16, C, 0, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn, R_ids,
-                                               (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta);
+               ? launch_gemm<uint16_t, C, CS, 0, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn,
+                                                     R_ids, (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta)
+               : launch_gemm<Half16, C, CS, 0, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn,
+                                                   R_ids, (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta);
   };
-  rc = cfg == 2 ? run(CfgHuge{}) : cfg == 1 ? run(CfgLarge{}) : run(CfgSmall{});
+  rc = cfg == 2 ? run(CfgHuge{}, TypeC<CfgShort>{}) : cfg == 1 ? run(CfgLarge{}, TypeC<void>{})
+                                                              : run(CfgSmall{}, TypeC<void>{});
   if (rc) return rc;
   return check_launch("grouped_gemm_kernel");
 }
