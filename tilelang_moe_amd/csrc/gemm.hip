@@ -34,6 +34,9 @@ constexpr int kScanThreads = 1024;
 // tall | short << 12: experts with at most `short` rows get one short tile,
 // the others tiles of `tall` rows.
 constexpr int32_t kShortTile = 1 << 30;
+// Byte offset of the grouped GEMM's nine schedule counters in the
+// workspace control block.
+constexpr size_t kGemmSchedOffset = 3072;
 
 // Bucket of routed row r.  Rows r < R_ids carry an expert id, valid in
 // [0, E_ids); rows r >= R_ids (an appended set, e.g. a shared expert taken
@@ -149,18 +152,25 @@ __device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int
   const int tall = bm & 0xFFF, shrt = bm >> 12;
   const int perE = (E + (int)blockDim.x - 1) / (int)blockDim.x;
   const int elo = std::min(E, tid * perE), ehi = std::min(E, elo + perE);
-  int32_t nt = 0;
+  // Tall tiles first, then the short ones (mixed tables): the GEMM's
+  // dynamic schedule then ends on the cheap tiles.
+  int32_t nt = 0, ns = 0;
   for (int e = elo; e < ehi; ++e) {
     const int32_t c = s_off[e + 1] - s_off[e];
-    nt += (c > 0 && c <= shrt) ? 1 : (c + tall - 1) / tall;
+    if (c > 0 && c <= shrt) ++ns;
+    else nt += (c + tall - 1) / tall;
   }
+  __shared__ int32_t s_tall_total;
   int32_t t = block_excl_scan(nt, wsum);
+  if (tid == (int)blockDim.x - 1) s_tall_total = t + nt;
+  int32_t ts = block_excl_scan(ns, wsum);  // its barriers also publish s_tall_total
+  ts += s_tall_total;
   for (int e = elo; e < ehi; ++e) {
     const int32_t c = s_off[e + 1] - s_off[e];
     if (c > 0 && c <= shrt) {
-      tile_expert[t] = e | kShortTile;
-      tile_mstart[t] = s_off[e];
-      ++t;
+      tile_expert[ts] = e | kShortTile;
+      tile_mstart[ts] = s_off[e];
+      ++ts;
       continue;
     }
     for (int32_t m = 0; m < c; m += tall, ++t) {
@@ -168,7 +178,7 @@ __device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int
       tile_mstart[t] = s_off[e] + m;
     }
   }
-  if (ehi == E && elo < ehi) meta[0] = t;  // the thread owning the last expert
+  if (tid == (int)blockDim.x - 1) meta[0] = ts;  // the last thread's short tiles end the table
 }
 
 // The tile table alone, for routing tables built by an earlier call for a
@@ -478,7 +488,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
     int64_t H, int64_t I, int topk, int64_t R, int E, int ntn, int64_t R_ids, int E_ids, int64_t x_shift,
     const int32_t* __restrict__ sorted_rows, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_mstart,
-    const int32_t* __restrict__ meta) {
+    const int32_t* __restrict__ meta, uint32_t* __restrict__ sched) {
   constexpr bool MIXED = !std::is_void<CfgS>::value;
   using CS = typename std::conditional<MIXED, CfgS, Cfg>::type;
   static_assert(CS::THREADS == Cfg::THREADS && CS::BN == Cfg::BN && CS::MINB == Cfg::MINB,
@@ -517,14 +527,47 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
   const int total = n_super_items + n_zero;
   // Otherwise (small problems) each XCD takes one contiguous eighth of the
   // list, its gridDim.x / 8 workgroups walking it in strides.
+  //
+  // In super-tile order with two tile heights the items are handed out
+  // dynamically: XCD x's queue holds super-tiles x, x + 8, ... in order,
+  // its workgroups take the next item from it with an atomic counter
+  // (sched[x]), and a workgroup whose queue is empty takes items from the
+  // other XCDs' queues.  Items differ in cost (tall tiles take about twice
+  // as long as short ones, which come last), so a static assignment left
+  // the last workgroups finishing hundreds of microseconds after the
+  // first.  The counters live in the workspace's control block: the last
+  // workgroup to finish (sched[8]) sets them back to zero.
   const bool by_super = by_super_raw;
+  const bool dynamic = MIXED && by_super;  // items of one height cost alike: static order
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int share = (total + 7) >> 3;
-  int w = by_super ? xcd * SUPER + slot : xcd * share + slot;
+  int w = dynamic ? -1 : by_super ? xcd * SUPER + slot : xcd * share + slot;
   const int w_end = by_super ? total : min(total, (xcd + 1) * share);
-  const int step = by_super ? (int)gridDim.x : (int)(gridDim.x >> 3);
-  for (; w < w_end; w += step) {
-    __syncthreads();  // the previous tile's LDS reads are done
+  const int step = dynamic ? 0 : by_super ? (int)gridDim.x : (int)(gridDim.x >> 3);
+  __shared__ int s_item;
+  int q = xcd;  // thread 0: the queue it drains
+  // Position p of XCD queue qq: item p % SUPER of super-tile 8 (p / SUPER) + qq.
+  auto item_of = [&](uint32_t p, int qq) -> int {
+    const int64_t cand = ((int64_t)(p / SUPER) * 8 + qq) * SUPER + p % SUPER;
+    return cand < total ? (int)cand : -1;
+  };
+  for (;; w += step) {
+    __syncthreads();  // the previous tile's LDS reads (and s_item reads) are done
+    if (dynamic) {
+      if (tid == 0) {
+        int item = item_of(atomicAdd(&sched[q], 1u), q);
+        for (int tried = 1; tried < 8 && item < 0; ++tried) {
+          q = (q + 1) & 7;  // queue q is empty: take from the next XCD's queue
+          item = item_of(atomicAdd(&sched[q], 1u), q);
+        }
+        s_item = item;
+      }
+      __syncthreads();
+      w = s_item;
+      if (w < 0) break;
+    } else if (w >= w_end) {
+      break;
+    }
     if (w >= n_super_items) {
       const int z = w - n_super_items;
       const int64_t z0 = (int64_t)offsets[E] + (int64_t)(z / ntn) * BM;
@@ -557,6 +600,11 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
       gemm_tile<T, Cfg, MODE, EPI>(smem, srow, X, W, W2, Wx, W2x, Y, H, I, topk, R_ids, E_ids, x_shift,
                                         sorted_rows, e, m0, mend, nt * OBN);
   }  // tile loop
+  if (dynamic && tid == 0 && atomicAdd(&sched[8], 1u) == gridDim.x - 1) {
+    // Every workgroup has found every queue empty: no counter is read again.
+#pragma unroll
+    for (int i = 0; i <= 8; ++i) sched[i] = 0;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -644,7 +692,7 @@ template <typename T, typename Cfg, typename CfgS, int MODE = 0, int EPI = 0>
 static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, const uint16_t* w2, const uint16_t* wx,
                        const uint16_t* w2x, uint16_t* y, int64_t H, int64_t I, int topk, int64_t R, int E, int ntn,
                        int64_t R_ids, int E_ids, int64_t x_shift, const int32_t* sorted, const int32_t* offsets,
-                       const int32_t* t_exp, const int32_t* t_ms, const int32_t* meta) {
+                       const int32_t* t_exp, const int32_t* t_ms, const int32_t* meta, uint32_t* sched) {
   using CS = typename std::conditional<std::is_void<CfgS>::value, Cfg, CfgS>::type;
   constexpr size_t lds = Cfg::LDS_BYTES > CS::LDS_BYTES ? Cfg::LDS_BYTES : CS::LDS_BYTES;
   static std::atomic<uint64_t> lds_cap_set{0};
@@ -654,7 +702,7 @@ static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, con
   const int64_t ub = ((R + Cfg::BM - 1) / Cfg::BM + E + 1) * ntn;  // tiles, upper bound
   const int64_t grid = ub >= 16 * Cfg::SUPER ? 8 * Cfg::SUPER : (ub + 7) / 8 * 8;
   grouped_gemm_kernel<T, Cfg, CfgS, MODE, EPI><<<dim3((unsigned)grid), Cfg::THREADS, lds, st>>>(
-      x, w, w2, wx, w2x, y, H, I, topk, R, E, ntn, R_ids, E_ids, x_shift, sorted, offsets, t_exp, t_ms, meta);
+      x, w, w2, wx, w2x, y, H, I, topk, R, E, ntn, R_ids, E_ids, x_shift, sorted, offsets, t_exp, t_ms, meta, sched);
   return MOE_OK;
 }
 
@@ -732,6 +780,9 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
     return fail(MOE_EINVAL, f + ": workspace too small (" + std::to_string(ws_bytes) + " < " +
                                 std::to_string(kWsCtlBytes + g.total) + ")");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // Dynamic-schedule counters of the GEMM kernel in the control block (zero
+  // before and after every call).
+  uint32_t* sched = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kGemmSchedOffset);
   char* ws = static_cast<char*>(workspace) + kWsCtlBytes;
   int32_t* blockcnt = reinterpret_cast<int32_t*>(ws + g.blockcnt);
   int32_t* counts = reinterpret_cast<int32_t*>(ws + g.counts);
@@ -774,9 +825,11 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
     using CS = typename decltype(cfgs_tag)::type;
     return dtype == MOE_BF16
                ? launch_gemm<uint16_t, C, CS, 0, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn,
-                                                     R_ids, (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta)
+                                                     R_ids, (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta,
+                                                     sched)
                : launch_gemm<Half16, C, CS, 0, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn,
-                                                   R_ids, (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta);
+                                                   R_ids, (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta,
+                                                   sched);
   };
   rc = cfg == 2 ? run(CfgHuge{}, TypeC<CfgShort>{}) : cfg == 1 ? run(CfgLarge{}, TypeC<void>{})
                                                               : run(CfgSmall{}, TypeC<void>{});
