@@ -402,7 +402,6 @@ __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* 
   // lane l fills slot l: row l / CPR, position l % CPR.
   constexpr int CPR = Cfg::CPR;
   const int crow = lane / CPR;
-  const int cchunk = (lane % CPR) ^ ((crow / (8 / CPR)) % CPR);
   const uint16_t* a_src[Cfg::A_INS];
   const uint16_t* b_src[Cfg::B_INS];
 #pragma unroll
@@ -411,18 +410,18 @@ __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* 
     const int sr = srow[r];
     // Rows past the expert's segment read X row 0; their results are never stored.
     const int64_t xr = sr < 0 ? 0 : (sr < R_ids ? sr / topk : sr - R_ids + x_shift);
-    a_src[i] = X + xr * H + cchunk * 8;
+    a_src[i] = X + xr * H + Cfg::copy_chunk(wave, i, Cfg::A_INS, lane) * 8;
   }
 #pragma unroll
   for (int i = 0; i < Cfg::B_INS; ++i) {
     const int nl = Cfg::RPI * (wave * Cfg::B_INS + i) + crow;  // tile row
     if constexpr (EPI == 0) {
       const int64_t n = n0 + nl;
-      b_src[i] = We + (n < I ? n : 0) * H + cchunk * 8;
+      b_src[i] = We + (n < I ? n : 0) * H + Cfg::copy_chunk(wave, i, Cfg::B_INS, lane) * 8;
     } else {
       const int blk = nl / 32;
       const int64_t n = n0 + (blk >> 1) * 32 + (nl & 31);
-      b_src[i] = ((blk & 1) ? W2e : We) + (n < I ? n : 0) * H + cchunk * 8;
+      b_src[i] = ((blk & 1) ? W2e : We) + (n < I ? n : 0) * H + Cfg::copy_chunk(wave, i, Cfg::B_INS, lane) * 8;
     }
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
@@ -439,7 +438,7 @@ __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* 
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  tile_mainloop<T, Cfg, MODE>(smem, a_src, b_src, cchunk, 0, H, fm_act, acc);
+  tile_mainloop<T, Cfg, MODE>(smem, a_src, b_src, 0, H, fm_act, acc);
 
   // Epilogue: accumulator v of lane l holds row 8*(v/4) + 4*(l/32) + v%4,
   // column l%32 of its 32x32 block.  Rows go back to their routed position.
@@ -820,14 +819,18 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   const uint16_t* wx = static_cast<const uint16_t*>(ex.Wx);
   const uint16_t* w2x = static_cast<const uint16_t*>(ex.W2x);
   uint16_t* y = static_cast<uint16_t*>(Y);
+  // MOE_GEMM_TUNE_MODE (tuning builds only): 1 = copies only, 2 = MFMAs only.
+#ifndef MOE_GEMM_TUNE_MODE
+#define MOE_GEMM_TUNE_MODE 0
+#endif
   auto run = [&](auto cfg_tag, auto cfgs_tag) {
     using C = decltype(cfg_tag);
     using CS = typename decltype(cfgs_tag)::type;
     return dtype == MOE_BF16
-               ? launch_gemm<uint16_t, C, CS, 0, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn,
+               ? launch_gemm<uint16_t, C, CS, MOE_GEMM_TUNE_MODE, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn,
                                                      R_ids, (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta,
                                                      sched)
-               : launch_gemm<Half16, C, CS, 0, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn,
+               : launch_gemm<Half16, C, CS, MOE_GEMM_TUNE_MODE, EPI>(st, x, w, w2, wx, w2x, y, H, I, (int)topk, R, (int)Et, ntn,
                                                    R_ids, (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta,
                                                    sched);
   };

@@ -62,18 +62,20 @@ __device__ inline void with_count(int n, Fn&& fn) {
 
 // Tile configurations.  A workgroup computes a BM x BN tile of one expert
 // with WM x WN waves, each owning FM x FN blocks of 32x32 (v_mfma 32x32x16);
-// K advances BK elements per pipeline stage and STAGES stages are in LDS.
+// K advances BK elements per k-tile and STAGES k-tiles are in LDS (STAGES-1
+// in flight while one is consumed).
 //
 // LDS layout of a stage: A rows then B rows, each row BK elements = CPR
 // chunks of 16 bytes.  Chunk c of row r sits at position
-//   c ^ ((r / (8 / CPR)) % CPR),
-// so the 8 lanes an LDS cycle serves in an MFMA operand fetch (8 consecutive
-// rows, one chunk each) hit 8 different 16-byte bank groups.
+//   c ^ ((r / SWZ) % CPR),   SWZ = 16 / CPR,
+// so the 16 lanes an LDS cycle serves in a 16-byte MFMA operand fetch (16
+// consecutive rows, one chunk each: 256 bytes over 64 four-byte banks) hit 16
+// different 16-byte bank groups.
 //
 // Global -> LDS copies are gfx950 global_load_lds_dwordx4: every lane
 // fetches one 16-byte chunk straight into LDS and a wave instruction fills
-// 1 KB (64 / CPR rows), so copies use no VGPRs and STAGES-1 k-tiles stay in
-// flight.  A lane picks the global chunk that belongs in its LDS slot.
+// 1 KB (64 / CPR rows), so copies use no VGPRs.  A lane picks the global
+// chunk that belongs in its LDS slot.
 template <int BM_, int BN_, int WM_, int WN_, int BK_, int STAGES_, int MINB_ = 1>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, BK = BK_, STAGES = STAGES_;
@@ -88,115 +90,157 @@ struct GemmCfg {
   static constexpr int STAGE_ELEMS = (BM + BN) * BK;
   static constexpr size_t LDS_BYTES = (size_t)STAGES * STAGE_ELEMS * 2;
   static_assert(CPR == 4 || CPR == 8, "BK must be 32 or 64");
+  static_assert(STAGES >= 2, "at least two stages");
   static_assert(FM >= 1 && FN >= 1 && A_INS >= 1 && B_INS >= 1, "bad tile configuration");
   static_assert(A_INS * WAVES * RPI == BM && B_INS * WAVES * RPI == BN, "rows must split evenly over waves");
   static_assert(LDS_BYTES + BM * 4 <= 160 * 1024, "LDS budget");
-  static __device__ inline int slot(int r, int c) { return r * CPR + (c ^ ((r / (8 / CPR)) % CPR)); }
+  static constexpr int SWZ = 16 / CPR;  // consecutive rows sharing one XOR key
+  // Position of chunk c in row r, and (XOR is an involution) the chunk that
+  // position c of row r holds.
+  static __device__ inline int pos(int r, int c) { return c ^ ((r / SWZ) % CPR); }
+  static __device__ inline int slot(int r, int c) { return r * CPR + pos(r, c); }
+  // The 16-byte chunk that lane `lane` copies in copy instruction `ins` of
+  // wave `wave` (INS instructions per wave): it fills position lane % CPR of
+  // operand row RPI * (wave * INS + ins) + lane / CPR.
+  static __device__ inline int copy_chunk(int wave, int ins, int INS, int lane) {
+    return pos(RPI * (wave * INS + ins) + lane / CPR, lane % CPR);
+  }
 };
+
 // The k loop of one output tile: acc[i][j] += A-rows x B-rows over k in
 // [kb, ke) (kb a multiple of BK; elements at k >= ke count as zero).
 // a_src / b_src are this thread's copy-slot row pointers, already offset by
-// its 16-byte chunk `cchunk`; fm_act is the wave-uniform count of 32-row
-// blocks of this wave that hold rows (the MFMAs of the others are skipped).
+// the 16-byte chunk of its slot (Cfg::copy_chunk); fm_act is the
+// wave-uniform count of 32-row blocks of this wave that hold rows (the
+// MFMAs of the others are skipped).  MODE (tuning builds only): 1 = copies
+// only, 2 = MFMAs only.
 template <typename T, typename Cfg, int MODE>
 __device__ inline void tile_mainloop(uint16_t* smem, const uint16_t* const (&a_src)[Cfg::A_INS],
-                                     const uint16_t* const (&b_src)[Cfg::B_INS], int cchunk, int64_t kb,
+                                     const uint16_t* const (&b_src)[Cfg::B_INS], int64_t kb,
                                      int64_t ke, int fm_act, f32x16 (&acc)[Cfg::FM][Cfg::FN]) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, S = Cfg::STAGES, CPR = Cfg::CPR;
+  constexpr int INS = Cfg::A_INS + Cfg::B_INS;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   const int nk = (int)((ke - kb + BK - 1) / BK);
   const bool ktail = ((ke - kb) % BK) != 0;
+  auto stage = [&](int t) { return smem + (t % S) * Cfg::STAGE_ELEMS; };
 
-  auto issue = [&](int kt) {
-    if (kt >= nk || MODE == 2) return;
-    uint16_t* st = smem + (kt % S) * Cfg::STAGE_ELEMS;
-    const int64_t k = kb + (int64_t)kt * BK;
-    // Chunks at or past ke (last k-tile only) read the row start; they are
-    // zeroed in LDS before use.
-    const int64_t koff = (k + cchunk * 8 < ke) ? k : -(int64_t)cchunk * 8;
+  // Copies of k-tile t into its stage.  Chunks at or past ke (last k-tile
+  // only) read the row start; they are zeroed in LDS before use.
+  auto issue = [&](int t) {
+    if (t >= nk || MODE == 2) return;
+    uint16_t* st = stage(t);
+    const int64_t k = kb + (int64_t)t * BK;
+    const bool tail = ktail && t == nk - 1;
+    auto koff = [&](int c) -> int64_t { return (!tail || k + c * 8 < ke) ? k : -(int64_t)c * 8; };
 #pragma unroll
     for (int i = 0; i < Cfg::A_INS; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + koff),
+      __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + koff(Cfg::copy_chunk(wave, i, Cfg::A_INS, lane))),
                                        (lds_void_t*)(st + (wave * Cfg::A_INS + i) * 512), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < Cfg::B_INS; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(b_src[i] + koff),
-                                       (lds_void_t*)(st + BM * BK + (wave * Cfg::B_INS + i) * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(b_src[i] + koff(Cfg::copy_chunk(wave, i, Cfg::B_INS, lane))),
+          (lds_void_t*)(st + BM * BK + (wave * Cfg::B_INS + i) * 512), 16, 0, 0);
   };
 
-#pragma unroll
-  for (int p = 0; p < S - 1; ++p) issue(p);
-
   // The k loop, specialised on the number FA of active 32-row blocks so
-  // that the skip is a scalar branch taken once per tile.  Per k-tile: wait
-  // for this thread's copies of the tile (the S-2 younger tiles stay in
-  // flight; the last tiles wait for all), barrier, refill the slot that
-  // k-tile kt-1 used, then BK/16 MFMA steps.  Operand fragments are double
-  // buffered in registers: the LDS reads of step s+1 are issued before the
-  // MFMAs of step s.
+  // that the skip is a scalar branch taken once per tile.
+  //
+  // Operand fragments are double buffered in registers: the LDS reads of
+  // step s+1 are issued between the MFMAs of step s.  The k-tile boundary
+  // sits inside the last step of a k-tile: once that step's fragments are
+  // in registers, the thread waits for its copies of the next k-tile (the
+  // S-2 younger k-tiles stay in flight), the workgroup meets at a barrier
+  // (every wave is then done reading the k-tile's stage and every copy of
+  // the next k-tile has landed), the freed stage is refilled, and the last
+  // step's MFMAs run while the next k-tile's first fragments are read.  So
+  // the MFMAs do not wait for a fresh LDS round trip after the barrier.
   auto k_loop = [&](auto fa_tag) {
     constexpr int FA = decltype(fa_tag)::value;
     constexpr int FAR = FA > 0 ? FA : 1;
     constexpr int STEPS = BK / 16;
-    for (int kt = 0; kt < nk; ++kt) {
-      if (kt + S - 2 < nk) vm_wait<(S - 2) * (Cfg::A_INS + Cfg::B_INS)>();
+    constexpr bool LOADS = FA > 0 || MODE == 1;
+    u32x4 a[2][FAR], b[2][Cfg::FN];
+    auto load = [&](int t, int s, int q) {
+      const u32x4* As = reinterpret_cast<const u32x4*>(stage(t));
+      const u32x4* Bs = reinterpret_cast<const u32x4*>(stage(t) + BM * BK);
+      const int c = 2 * s + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < FA; ++i) a[q][i] = As[Cfg::slot(wm * Cfg::FM * 32 + i * 32 + (lane & 31), c)];
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j) b[q][j] = Bs[Cfg::slot(wn * Cfg::FN * 32 + j * 32 + (lane & 31), c)];
+    };
+    auto mfmas = [&](int q) {
+      if constexpr (MODE == 1) {
+        acc[0][0][0] += __uint_as_float(a[q][0][0] ^ b[q][0][0]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < FA; ++i)
+#pragma unroll
+          for (int j = 0; j < Cfg::FN; ++j) acc[i][j] = MfmaOp<T>::run(a[q][i], b[q][j], acc[i][j]);
+      }
+    };
+    // Pins one step's order: each MFMA followed by one of the next reads.
+    auto pin_step = [&]() {
+      if constexpr (MODE != 1 && FA > 0) {
+#pragma unroll
+        for (int m = 0; m < FA * Cfg::FN; ++m) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (m < FA + Cfg::FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
+    };
+    // Make k-tile t visible to the workgroup and refill the stage of t-1.
+    auto arrive = [&](int t) {
+      if (t + S - 2 < nk) vm_wait<(S - 2) * INS>();
       else vm_wait<0>();
       // Plain s_barrier: __syncthreads() would also wait for the younger
       // k-tiles still in flight (its release fence drains vmcnt).
       __builtin_amdgcn_s_barrier();
-      issue(kt + S - 1);
-      const uint16_t* st = smem + (kt % S) * Cfg::STAGE_ELEMS;
-      if (ktail && kt == nk - 1) {
+      issue(t + S - 1);
+      if (ktail && t == nk - 1) {
         // Zero the chunks at or past ke of the last k-tile in both operands.
-        uint16_t* sw = const_cast<uint16_t*>(st);
-        const int64_t k = kb + (int64_t)kt * BK;
+        uint16_t* sw = stage(t);
+        const int64_t k = kb + (int64_t)t * BK;
         for (int q = tid; q < (BM + BN) * CPR; q += Cfg::THREADS) {
-          const int r = q / CPR, pos = q % CPR, c = pos ^ ((r / (8 / CPR)) % CPR);
+          const int r = q / CPR, c = Cfg::pos(r, q % CPR);
           if (k + c * 8 >= ke) *reinterpret_cast<u32x4*>(sw + q * 8) = u32x4{0u, 0u, 0u, 0u};
         }
         __syncthreads();
       }
-      const u32x4* As = reinterpret_cast<const u32x4*>(st);
-      const u32x4* Bs = reinterpret_cast<const u32x4*>(st + BM * BK);
-      u32x4 a[2][FAR], b[2][Cfg::FN];
-      auto load = [&](int s, int q) {
-        const int c = 2 * s + (lane >> 5);
+    };
+
+    if (nk <= 0) return;
 #pragma unroll
-        for (int i = 0; i < FA; ++i) a[q][i] = As[Cfg::slot(wm * Cfg::FM * 32 + i * 32 + (lane & 31), c)];
+    for (int t = 0; t < S - 1; ++t) issue(t);
+    arrive(0);
+    if constexpr (LOADS) load(0, 0, 0);
+    // Steps 0 .. STEPS-2 of k-tile t (the last step differs per k-tile).
+    auto front = [&](int t) {
 #pragma unroll
-        for (int j = 0; j < Cfg::FN; ++j) b[q][j] = Bs[Cfg::slot(wn * Cfg::FN * 32 + j * 32 + (lane & 31), c)];
-      };
-      if constexpr (FA > 0 || MODE == 1) load(0, 0);
-#pragma unroll
-      for (int s = 0; s < STEPS; ++s) {
-        if constexpr (FA > 0 || MODE == 1)
-          if (s + 1 < STEPS) load(s + 1, (s + 1) & 1);
-        if constexpr (MODE == 1) {
-          acc[0][0][0] += __uint_as_float(a[s & 1][0][0] ^ b[s & 1][0][0]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < FA; ++i)
-#pragma unroll
-            for (int j = 0; j < Cfg::FN; ++j) acc[i][j] = MfmaOp<T>::run(a[s & 1][i], b[s & 1][j], acc[i][j]);
-        }
+      for (int s = 0; s + 1 < STEPS; ++s) {
+        if constexpr (LOADS) load(t, s + 1, (s + 1) & 1);
+        mfmas(s & 1);
       }
-      if constexpr (MODE != 1 && FA > 0) {
-        // Instruction order of the k-tile: step 0's LDS reads, then each
-        // step's MFMAs with the next step's reads placed one after each
-        // MFMA, so those reads are in flight while the MFMAs run.
-        __builtin_amdgcn_sched_group_barrier(0x100, FA + Cfg::FN, 0);
 #pragma unroll
-        for (int s = 0; s < STEPS; ++s)
-#pragma unroll
-          for (int m = 0; m < FA * Cfg::FN; ++m) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (s + 1 < STEPS && m < FA + Cfg::FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          }
-      }
+      for (int s = 0; s + 1 < STEPS; ++s) pin_step();
+    };
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+      front(kt);
+      // The last step's fragments are in registers before the barrier, so
+      // after it the stage of k-tile kt may be overwritten.
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      arrive(kt + 1);
+      if constexpr (LOADS) load(kt + 1, 0, 0);
+      mfmas((STEPS - 1) & 1);
+      pin_step();
     }
+    front(nk - 1);
+    mfmas((STEPS - 1) & 1);
   };
   with_count<Cfg::FM>(fm_act, k_loop);
 }

@@ -117,18 +117,17 @@ __global__ __launch_bounds__(Cfg::THREADS) void router_gemm_kernel(
   // instruction.  Rows past T and columns past E read row 0; their results
   // are never stored.
   const int crow = lane / CPR;
-  const int cchunk = (lane % CPR) ^ ((crow / (8 / CPR)) % CPR);
   const uint16_t* a_src[Cfg::A_INS];
   const uint16_t* b_src[Cfg::B_INS];
 #pragma unroll
   for (int i = 0; i < Cfg::A_INS; ++i) {
     const int64_t r = m0 + Cfg::RPI * (wave * Cfg::A_INS + i) + crow;
-    a_src[i] = X + (r < Tn ? r : 0) * H + cchunk * 8;
+    a_src[i] = X + (r < Tn ? r : 0) * H + Cfg::copy_chunk(wave, i, Cfg::A_INS, lane) * 8;
   }
 #pragma unroll
   for (int i = 0; i < Cfg::B_INS; ++i) {
     const int n = n0 + Cfg::RPI * (wave * Cfg::B_INS + i) + crow;
-    b_src[i] = Wt + (int64_t)(n < E ? n : 0) * H + cchunk * 8;
+    b_src[i] = Wt + (int64_t)(n < E ? n : 0) * H + Cfg::copy_chunk(wave, i, Cfg::B_INS, lane) * 8;
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   const int mcount = (int)min((int64_t)BM, Tn - m0);
@@ -140,7 +139,7 @@ __global__ __launch_bounds__(Cfg::THREADS) void router_gemm_kernel(
     for (int j = 0; j < Cfg::FN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-  tile_mainloop<T, Cfg, 0>(smem, a_src, b_src, cchunk, kb, ke, fm_act, acc);
+  tile_mainloop<T, Cfg, 0>(smem, a_src, b_src, kb, ke, fm_act, acc);
 
   // Accumulator v of lane l: row 8*(v/4) + 4*(l/32) + v%4, column l%32 of
   // its 32x32 block.
