@@ -185,6 +185,23 @@ int moe_grouped_gemm_routed(const void* X, const void* W, int dtype, int64_t T,
                             int64_t topk, int64_t H, int64_t I, int64_t E, void* Y,
                             void* workspace, size_t ws_bytes, void* stream);
 
+/* moe_grouped_gemm without the workspace arguments; it calls no allocating
+ * routine.  It has no counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  The workspace lives in a
+ * file-scope device array of MOE_NOALLOC_SCRATCH_BYTES per device, held
+ * from the first call on a device until the process ends.  Problems whose
+ * workspace (moe_grouped_gemm_workspace_size) exceeds it are rejected with
+ * MOE_EUNSUP (beyond about 990K routed rows at E = 256, 740K at E = 4096).  All
+ * calls on one device share the array: calls that overlap in time on one
+ * device (concurrent streams, or host threads) race and must not be
+ * issued.  The current device must be the stream's device.  Arguments as
+ * moe_grouped_gemm. */
+#define MOE_NOALLOC_SCRATCH_BYTES (4u << 20)
+int moe_grouped_gemm_noalloc(const void* X, const void* W, const void* expert_ids,
+                             int dtype, int idx_dtype, int64_t T, int64_t topk,
+                             int64_t H, int64_t I, int64_t E, void* Y, void* stream);
+
 /* ---------------------------------------------------------------------
  * Router GEMM (logits = X . W) and the fused router GEMM + TopK + softmax.
  * The weights are used transposed, Wt [E, H], so that both MFMA operands

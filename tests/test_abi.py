@@ -124,3 +124,17 @@ def test_router_python_api_shapes_and_names():
         R.router_topk_softmax(torch.randn(4, 16).bfloat16(), torch.randn(16, 8).bfloat16(), 2)
     for algo in R.FUSED_ALGOS:
         assert callable(getattr(R, f"fused_router_{algo}_kernel")(256, 4096, 160, 256, 8))
+
+
+def test_noalloc_host_checks():
+    L = _lib.lib()
+    m = re.search(r"#define MOE_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", open(HEADER).read())
+    assert m and int(m[1]) << int(m[2]) == _lib.MOE_NOALLOC_SCRATCH_BYTES
+    # T == 0 is a no-op; bad shapes and problems beyond the fixed scratch are
+    # rejected before any device call.
+    assert L.moe_grouped_gemm_noalloc(None, None, None, 1, 3, 0, 8, 64, 64, 256, None, None) == _lib.MOE_OK
+    assert L.moe_grouped_gemm_noalloc(16, 16, 16, 1, 3, 4, 0, 64, 64, 8, 16, None) == _lib.MOE_EINVAL
+    assert L.moe_grouped_gemm_noalloc(16, 16, 16, 1, 3, 4, 1, 64, 64, 5000, 16, None) == _lib.MOE_EUNSUP
+    assert L.moe_grouped_gemm_noalloc(16, 16, 16, 1, 3, 200000, 8, 64, 64, 256, 16, None) == _lib.MOE_EUNSUP
+    assert b"scratch" in L.moe_last_error()
+    assert L.moe_grouped_gemm_workspace_size(200000, 8, 256, 64) > _lib.MOE_NOALLOC_SCRATCH_BYTES

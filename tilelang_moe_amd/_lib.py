@@ -18,6 +18,7 @@ MOE_F32, MOE_BF16, MOE_F16, MOE_I32, MOE_I64 = 0, 1, 2, 3, 4
 MOE_TOPK_AUTO, MOE_TOPK_BITONIC, MOE_TOPK_SELECTION, MOE_TOPK_RADIX = -1, 0, 1, 2
 MOE_OK, MOE_EINVAL, MOE_EUNSUP, MOE_EHIP = 0, -1, -2, -3
 MOE_SCORES_TOPK, MOE_SCORES_ALL, MOE_SCORES_TOPK_RENORM = 0, 1, 2
+MOE_NOALLOC_SCRATCH_BYTES = 4 << 20  # include/moe_hip.h
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -42,6 +43,8 @@ SIGNATURES = {
                                   _c_i64, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
     "moe_grouped_gemm_routed": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                          _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "moe_grouped_gemm_noalloc": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_i64, _c_i64, _c_i64,
+                                          _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "moe_grouped_gemm_swiglu": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_i64, _c_i64,
                                          _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
     "moe_combine": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),

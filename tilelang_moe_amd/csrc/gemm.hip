@@ -20,6 +20,7 @@
 #include "mfma_tile.h"
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -873,4 +874,70 @@ extern "C" int moe_grouped_gemm_routed(const void* X, const void* W, int dtype, 
   ex.reuse_bm = -1;  // the routing tables of the previous call of this shape on this workspace
   return grouped_gemm_impl<0>("grouped_gemm_routed", X, W, nullptr, nullptr, dtype, MOE_I32, T, topk, H, I, E, ex, Y,
                               workspace, ws_bytes, stream, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// moe_grouped_gemm_noalloc: moe_grouped_gemm with its workspace in a
+// file-scope device array, for callers that cannot allocate.
+// ---------------------------------------------------------------------------
+namespace moe {
+
+// The workspace of moe_grouped_gemm_noalloc (control block + routing
+// tables).  Every device holds its own copy for the life of the process and
+// every call on a device uses that device's copy.  In host code the name
+// `scratch` is only a handle: kernels get the address that
+// hipGetSymbolAddress returns (noalloc_scratch), never the symbol itself.
+static __device__ __align__(256) unsigned char scratch[MOE_NOALLOC_SCRATCH_BYTES];
+
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+
+// Device address of the current device's `scratch`, looked up on the first
+// call on that device (with that device current) and kept.
+static int noalloc_scratch(void** out) {
+  int dev = 0;
+  MOE_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MOE_EUNSUP, "grouped_gemm_noalloc: device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    MOE_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(MOE_EHIP, "grouped_gemm_noalloc: hipGetSymbolAddress returned a null address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOE_OK;
+}
+
+}  // namespace moe
+
+extern "C" int moe_grouped_gemm_noalloc(const void* X, const void* W, const void* expert_ids, int dtype,
+                                        int idx_dtype, int64_t T, int64_t topk, int64_t H, int64_t I, int64_t E,
+                                        void* Y, void* stream) {
+  if (T < 0 || topk < 1 || H < 1 || I < 1) return fail(MOE_EINVAL, "grouped_gemm_noalloc: need T >= 0, topk >= 1, H >= 1, I >= 1");
+  if (E < 1 || E > kMaxExperts) return fail(MOE_EUNSUP, "grouped_gemm_noalloc: need 1 <= E <= 4096");
+  if (T == 0) return MOE_OK;
+  if (T > (int64_t)INT32_MAX / topk) return fail(MOE_EUNSUP, "grouped_gemm_noalloc: problem too large");
+  const size_t need = kWsCtlBytes + gemm_layout(T * topk, E).total;
+  if (need > (size_t)MOE_NOALLOC_SCRATCH_BYTES)
+    return fail(MOE_EUNSUP, "grouped_gemm_noalloc: " + std::to_string(T * topk) + " routed rows over " +
+                                std::to_string(E) + " experts need " + std::to_string(need) +
+                                " bytes of scratch, more than its fixed " +
+                                std::to_string((size_t)MOE_NOALLOC_SCRATCH_BYTES) +
+                                "; use moe_grouped_gemm with a workspace");
+  void* ws = nullptr;
+  if (int rc = noalloc_scratch(&ws)) return rc;
+  // The control block must be zero; every completed call leaves it so, and
+  // this clears it after a call that stopped part-way.  A kernel, not
+  // hipMemsetAsync, so that the call can be captured into a HIP graph.
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  zero_words_kernel<<<1, 256, 0, st>>>(static_cast<uint32_t*>(ws), (int)(kWsCtlBytes / 4));
+  if (int rc = check_launch("zero_words_kernel")) return rc;
+  return grouped_gemm_impl<0>("grouped_gemm_noalloc", X, W, nullptr, expert_ids, dtype, idx_dtype, T, topk, H, I, E,
+                              GemmExtra{}, Y, ws, (size_t)MOE_NOALLOC_SCRATCH_BYTES, stream, nullptr);
 }
