@@ -157,6 +157,19 @@ def test_fusedmoe_large(cuda, T, Dh, De, Ds, E, k):
     torch.testing.assert_close(out.float(), torch_moe_ref(x, w, k, wts, ids.long()), rtol=2e-2, atol=2e-2)
 
 
+@pytest.mark.parametrize("T", [40, 600])  # split-H and unsplit router GEMM
+def test_fusedmoe_more_than_256_experts(cuda, T):
+    """E > 256: the router runs as router GEMM + TopK (the fused router
+    selection stops at 256 experts)."""
+    E, k = 288, 8
+    x, w = _moe_weights(T, 512, 128, 128, E, seed=E + T)
+    out, wts, ids = K.fused_moe_routed(x, **w, n_experts_per_token=k, return_routing=True)
+    torch.cuda.synchronize()
+    assert int(ids.max()) < E and int(ids.min()) >= 0
+    check_routing(x, w["router_weight"], k, wts, ids)
+    torch.testing.assert_close(out.float(), torch_moe_ref(x, w, k, wts, ids.long()), rtol=2e-2, atol=2e-2)
+
+
 def test_reference_signatures(cuda):
     B, S, Dh, De, E, k = 2, 64, 256, 128, 8, 2
     x, w = _moe_weights(B * S, Dh, De, De, E, seed=5)

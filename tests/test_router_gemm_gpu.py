@@ -184,8 +184,9 @@ def test_empty_and_repeated_calls(cuda):
 
 
 def test_strided_weight_view(cuda):
-    """W given as a transposed view (unit row stride, column stride H): the
-    wrappers make it unit-column-stride before the transpose kernel reads it."""
+    """W given as a transposed view (unit row stride, column stride H): its
+    first E rows are already the kernels' layout and are read in place (no
+    copy, no cache entry), with the same results as the contiguous W."""
     g = torch.Generator(device="cuda").manual_seed(7)
     T, H, E, k = 96, 512, 48, 6
     X = torch.randn(T, H, generator=g, device="cuda").bfloat16()
@@ -196,6 +197,15 @@ def test_strided_weight_view(cuda):
     for a, b in zip(K.router_topk_softmax(X, W_view, k), K.router_topk_softmax(X, W, k)):
         assert torch.equal(a, b)
     assert torch.equal(K.router_gemm(X, W_view), K.router_gemm(X, W))
+    Wt = R.transposed_weight(W_view, E)
+    assert Wt.data_ptr() == Wt_full.data_ptr() and Wt.is_contiguous()
+    # A padded transposed view (E of E + 16 rows) reads the first E rows.
+    Wt_pad = (torch.randn(E + 16, H, generator=g, device="cuda") / H ** 0.5).bfloat16()
+    assert torch.equal(K.router_gemm(X, Wt_pad.t(), E), K.router_gemm(X, Wt_pad[:E].t().contiguous()))
+    # Neither unit stride: one contiguous copy, transposed.
+    W_odd = Wt_full.t()[::2]  # [H/2, E], strides (2, H)
+    X2 = X[:, : H // 2].contiguous()
+    assert torch.equal(K.router_gemm(X2, W_odd), K.router_gemm(X2, W_odd.contiguous()))
 
 
 @pytest.mark.parametrize("E,k", [(64, 8), (300, 4)])  # fused kernel; beyond the fused limit (two launches)
@@ -221,3 +231,10 @@ def test_weight_transpose_exact(cuda, H, E):
     assert torch.equal(K.prepare_router_weight(W), W.t().contiguous())
     Wpad = torch.randn(H, E + 8, device="cuda").bfloat16()  # padded columns past E (row stride E + 8)
     assert torch.equal(K.prepare_router_weight(Wpad, E), Wpad[:, :E].t().contiguous())
+    # Odd row stride E + 1, and a start 2 bytes past a 16-byte boundary: the
+    # 16-byte transpose path must not be taken for either.
+    base = torch.randn(H, E + 1, device="cuda").bfloat16()
+    assert torch.equal(K.prepare_router_weight(base[:, :E]), base[:, :E].t().contiguous())
+    W_mis = base[:, 1:E + 1]
+    assert W_mis.data_ptr() % 16 != 0
+    assert torch.equal(K.prepare_router_weight(W_mis), W_mis.t().contiguous())

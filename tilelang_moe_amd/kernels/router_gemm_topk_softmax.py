@@ -85,6 +85,18 @@ def transposed_weight(W: torch.Tensor, E: int) -> torch.Tensor:
     cached): every replay then reads W as it is at replay time, as the
     reference's kernels do."""
     H = W.shape[0]
+    if W.stride(0) == 1 and W.stride(1) == H and (W.data_ptr() % 16) == 0:
+        # W is the transposed view of a contiguous [>=E, H] tensor: its first
+        # E rows are already the kernels' layout and are read in place.
+        return W.t()[:E]
+    if W.stride(1) != 1:
+        # Other layouts: one contiguous copy, transposed, not cached (the
+        # copy's storage would make a new cache key on every call).
+        W = W.contiguous()
+        Wt = torch.empty((E, H), dtype=W.dtype, device=W.device)
+        _lib.check(_lib.lib().moe_router_weight_transpose(W.data_ptr(), _DTYPES[W.dtype], H, E, W.stride(0),
+                                                          Wt.data_ptr(), _lib.current_stream(W.device)))
+        return Wt
     capturing = torch.cuda.is_current_stream_capturing()
     key = (W.device.index, W.untyped_storage().data_ptr(), W.storage_offset(), W._version,
            tuple(W.shape), tuple(W.stride()), W.dtype, E)
@@ -109,7 +121,7 @@ def transposed_weight(W: torch.Tensor, E: int) -> torch.Tensor:
 
 def _check(X: torch.Tensor, W: torch.Tensor, E: int) -> Tuple[torch.Tensor, torch.Tensor, int, int]:
     """Validates X [T, H] and W [H, >=E]; returns (X, W, T, H) with X
-    contiguous and W of unit column stride (what the transpose reads)."""
+    contiguous (W keeps its layout: transposed_weight handles any)."""
     if not isinstance(X, torch.Tensor) or not isinstance(W, torch.Tensor):
         raise TypeError("X and W must be torch.Tensors")
     if X.dim() != 2 or W.dim() != 2:
@@ -123,8 +135,6 @@ def _check(X: torch.Tensor, W: torch.Tensor, E: int) -> Tuple[torch.Tensor, torc
         raise ValueError(f"hidden size mismatch: X has H={H}, W has {W.shape[0]} rows")
     if not 1 <= E <= W.shape[1]:
         raise ValueError(f"E={E} must be in [1, {W.shape[1]}]")
-    if W.stride(1) != 1:
-        W = W.contiguous()
     X = X.contiguous()
     return X, W, T, H
 
@@ -137,6 +147,8 @@ def prepare_router_weight(W: torch.Tensor, E: int = None) -> torch.Tensor:
     result is a snapshot of W."""
     E = W.shape[1] if E is None else int(E)
     _, W, _, H = _check(W.new_empty((0, W.shape[0])), W, E)
+    if W.stride(1) != 1:
+        W = W.contiguous()
     Wt = torch.empty((E, H), dtype=W.dtype, device=W.device)
     _lib.check(_lib.lib().moe_router_weight_transpose(W.data_ptr(), _DTYPES[W.dtype], H, E, W.stride(0),
                                                       Wt.data_ptr(), _lib.current_stream(W.device)))
