@@ -795,7 +795,13 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   // (BK 64, full 128-byte lines per row copy) moves the least data per
   // MFMA; smaller problems take smaller tiles to fill the chip.
   auto tiles_of = [&](int64_t bm, int64_t bn) { return ((R + bm - 1) / bm) * ((Iv + bn - 1) / bn); };
-  const int cfg = tiles_of(CfgHuge::BM, CfgHuge::BN) >= 512 ? 2 : tiles_of(CfgLarge::BM, CfgLarge::BN) >= 512 ? 1 : 0;
+  // Also the mixed 256/128-row configuration when experts average at most
+  // 128 rows and there are enough 128x256 tiles for every CU: each expert
+  // is then one short tile per N tile, streaming its weights once.
+  const bool short_experts = R <= 128 * Et && tiles_of(CfgShort::BM, CfgShort::BN) >= 256;
+  const int cfg = tiles_of(CfgHuge::BM, CfgHuge::BN) >= 512 || short_experts ? 2
+                  : tiles_of(CfgLarge::BM, CfgLarge::BN) >= 512              ? 1
+                                                                             : 0;
   const int bm = cfg == 2 ? CfgHuge::BM | CfgShort::BM << 12 : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
   const int bn = cfg == 2 ? CfgHuge::BN : cfg == 1 ? CfgLarge::BN : CfgSmall::BN;
   if (bm_used) *bm_used = bm;
