@@ -85,12 +85,13 @@ def build_fast() -> str:
     if cxx is None:
         raise RuntimeError("no C++ compiler (g++) found for the torch binding")
     abi = int(bool(getattr(torch._C, "_GLIBCXX_USE_CXX11_ABI", True)))
-    inc = [f"-I{p}" for p in ce.include_paths()] + [f"-I{sysconfig.get_paths()['include']}"]
+    inc = [f"-I{p}" for p in ce.include_paths()] + [f"-I{sysconfig.get_paths()['include']}", "-I/opt/rocm/include"]
     libs = [f"-L{p}" for p in ce.library_paths()] + [f"-Wl,-rpath,{p}" for p in ce.library_paths()]
     tmp = FAST_PATH + ".tmp"
     cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-w", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
            f"-DTORCH_EXTENSION_NAME={FAST_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H", *inc,
-           os.path.join(CSRC, "torch_bind.cpp"), "-o", tmp, *libs, "-lc10", "-ltorch", "-ltorch_cpu",
+           os.path.join(CSRC, "torch_bind.cpp"), "-o", tmp, *libs, "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
            "-ltorch_python"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

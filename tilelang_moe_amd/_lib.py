@@ -169,13 +169,9 @@ def _grow(dev_index: int, stream: int, nbytes: int):
         cache[key] = ent
         if capturing:
             _ws_retired.append(buf)  # graph-pool memory: never released by this package
+        elif fast is not None:
+            fast.set_workspace(dev_index, stream, ent[1], size)  # the router call looks it up in C++
         return ent
-
-
-def workspace_entry(dev_index: int, stream: int):
-    """(data_ptr, bytes) of the current workspace of (dev_index, stream), or (0, 0)."""
-    ent = _ws_cache.get((dev_index, stream))
-    return (ent[1], ent[2]) if ent is not None else (0, 0)
 
 
 def workspace(dev, stream: int, nbytes: int):

@@ -8,15 +8,19 @@
 // reference's exception type, through pybind11's std::invalid_argument
 // mapping), allocates the outputs with at::empty and calls the C ABI
 // through addresses handed over once by bind() (from the ctypes handle that
-// loaded the library), so this module links against neither the library
-// nor HIP.  Nonzero return codes are turned into exceptions by the Python
+// loaded the library), so this module does not link the library.  The
+// router call also takes torch's current stream and the stream's cached
+// workspace here (set_workspace), so that the Python wrapper makes a single
+// call.  Nonzero return codes are turned into exceptions by the Python
 // wrappers (the C ABI's thread-local message is read via ctypes).
 #include <torch/extension.h>
+#include <c10/hip/HIPStream.h>
 
 #include <cstdint>
 #include <stdexcept>
 #include <string>
 #include <tuple>
+#include <vector>
 
 namespace {
 
@@ -30,6 +34,24 @@ topk_fn g_topk = nullptr;
 gemm_fn g_gemm = nullptr;
 ws_fn g_topk_ws = nullptr;
 
+// Workspaces made outside graph capture, per (device, raw stream): the same
+// buffers the Python side keeps alive (tilelang_moe_amd/_lib.py).  Calls
+// come with the GIL held, so the table needs no lock.
+struct WsEntry {
+  int64_t dev, stream, ptr, bytes;
+};
+std::vector<WsEntry> g_ws;
+
+void set_workspace(int64_t dev, int64_t stream, int64_t ptr, int64_t bytes) {
+  for (auto& e : g_ws)
+    if (e.dev == dev && e.stream == stream) {
+      e.ptr = ptr;
+      e.bytes = bytes;
+      return;
+    }
+  g_ws.push_back({dev, stream, ptr, bytes});
+}
+
 void bind(int64_t topk_addr, int64_t gemm_addr, int64_t topk_ws_addr) {
   if (!topk_addr || !gemm_addr || !topk_ws_addr) throw std::invalid_argument("bind: null function address");
   g_topk = reinterpret_cast<topk_fn>(static_cast<intptr_t>(topk_addr));
@@ -39,14 +61,16 @@ void bind(int64_t topk_addr, int64_t gemm_addr, int64_t topk_ws_addr) {
 
 // Drop-in TopK + softmax: validates like the Python wrappers of the
 // reference (ValueError for bad arguments), allocates the outputs and calls
-// moe_topk_softmax_ex.  Returns (return code, workspace bytes needed,
-// scores or None, indices); when the caller's workspace (ws, ws_bytes) is
-// smaller than the call needs, nothing is launched and the code is -100.
+// moe_topk_softmax_ex on torch's current stream of the logits' device.
+// Returns (return code, workspace bytes needed, scores or None, indices).
+// The workspace is (ws, ws_bytes) when ws >= 0, else the stream's entry of
+// set_workspace; when it is smaller than the call needs, nothing is
+// launched and the code is -100.
 constexpr int64_t kNeedWorkspace = -100;
 
 std::tuple<int64_t, int64_t, c10::optional<at::Tensor>, at::Tensor> topk_softmax(
     const at::Tensor& logits_in, int64_t k, int64_t algo, bool with_scores, bool idx64, int64_t score_mode,
-    int64_t ws, int64_t ws_bytes, int64_t stream) {
+    int64_t ws, int64_t ws_bytes) {
   if (!g_topk) throw std::runtime_error("_moe_torch: bind() has not been called");
   if (logits_in.dim() != 2)
     throw std::invalid_argument("logits must be 2-D [num_tokens, num_experts], got shape " +
@@ -64,6 +88,17 @@ std::tuple<int64_t, int64_t, c10::optional<at::Tensor>, at::Tensor> topk_softmax
                                 std::to_string(k));
   const at::Tensor logits =
       (logits_in.stride(1) != 1 || logits_in.stride(0) < n) ? logits_in.contiguous() : logits_in;
+  const int64_t dev = logits.get_device();
+  const int64_t stream = reinterpret_cast<int64_t>(c10::hip::getCurrentHIPStream(dev).stream());
+  if (ws < 0) {
+    ws = ws_bytes = 0;
+    for (const auto& e : g_ws)
+      if (e.dev == dev && e.stream == stream) {
+        ws = e.ptr;
+        ws_bytes = e.bytes;
+        break;
+      }
+  }
   const int64_t need = m > 0 ? static_cast<int64_t>(g_topk_ws(m, n, k, static_cast<int>(algo))) : 0;
   if (need > ws_bytes) return {kNeedWorkspace, need, c10::nullopt, at::Tensor()};
   at::Tensor idx = at::empty({m, k}, logits.options().dtype(idx64 ? at::kLong : at::kInt));
@@ -98,6 +133,9 @@ std::tuple<int64_t, at::Tensor> grouped_gemm(const at::Tensor& X, const at::Tens
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("bind", &bind,
         "Take the addresses of moe_topk_softmax_ex, moe_grouped_gemm and moe_topk_softmax_workspace_size.");
-  m.def("topk_softmax", &topk_softmax, "moe_topk_softmax_ex with outputs allocated here.");
+  m.def("set_workspace", &set_workspace, "Record the workspace of (device, raw stream) for topk_softmax.");
+  m.def("topk_softmax", &topk_softmax, "moe_topk_softmax_ex with outputs allocated here.", py::arg("logits"),
+        py::arg("k"), py::arg("algo"), py::arg("with_scores"), py::arg("idx64"), py::arg("score_mode"),
+        py::arg("ws") = -1, py::arg("ws_bytes") = 0);
   m.def("grouped_gemm", &grouped_gemm, "moe_grouped_gemm with the output allocated here.");
 }

@@ -54,15 +54,12 @@ def _run(logits: torch.Tensor, k, algo: int, with_scores: bool,
     if k.__class__ is not int:
         k = int(k.item()) if isinstance(k, torch.Tensor) else int(k)
     fast = _lib.fast or (_lib.lib(), _lib.fast)[1]
-    didx = logits.get_device()
-    stream = _raw_stream(didx) if didx >= 0 else 0
-    ws, ws_bytes = _lib.workspace_entry(didx, stream)
-    rc, need, scores, indices = fast.topk_softmax(logits, k, algo, with_scores, index_dtype is torch.int64,
-                                                  score_mode, ws, ws_bytes, stream)
+    idx64 = index_dtype is torch.int64
+    rc, need, scores, indices = fast.topk_softmax(logits, k, algo, with_scores, idx64, score_mode)
     if rc == _NEED_WORKSPACE:
-        ws = _lib.workspace_ptr(didx, stream, need)
-        rc, need, scores, indices = fast.topk_softmax(logits, k, algo, with_scores, index_dtype is torch.int64,
-                                                      score_mode, ws, need, stream)
+        didx = logits.get_device()
+        ws = _lib.workspace_ptr(didx, _raw_stream(didx), need)
+        rc, need, scores, indices = fast.topk_softmax(logits, k, algo, with_scores, idx64, score_mode, ws, need)
     if rc:
         _lib.check(rc)
     return scores, indices
