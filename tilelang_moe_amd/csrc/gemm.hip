@@ -145,12 +145,20 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
 // The M-tile table for tile height bm from segment offsets already in LDS
 // (s_off[0..E], published by a barrier): expert e owns ceil(count_e / bm)
 // consecutive M tiles, or one short tile when bm = tall | short << 12 and
-// count_e <= short; meta[0] = number of tiles.  One block (any size).
+// count_e <= short; meta[0] = number of table entries.  One block (any
+// size).
+//
+// With bm = tall | short << 12 | blk << 24 (blk > 0) the tall and the short
+// tiles alternate in blocks of blk entries (T S T S ..., the longer list's
+// remainder last), so that a GEMM that walks the table in super-tiles of
+// blk M tiles runs weight-streaming short tiles beside compute-heavy tall
+// ones.  A partial block that another block follows leaves holes, marked
+// tile_expert = -1.
 __device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int32_t* wsum,
                                         int32_t* __restrict__ tile_expert, int32_t* __restrict__ tile_mstart,
                                         int32_t* __restrict__ meta) {
   const int tid = threadIdx.x;
-  const int tall = bm & 0xFFF, shrt = bm >> 12;
+  const int tall = bm & 0xFFF, shrt = (bm >> 12) & 0xFFF, blk = (bm >> 24) & 0x3F;
   const int perE = (E + (int)blockDim.x - 1) / (int)blockDim.x;
   const int elo = std::min(E, tid * perE), ehi = std::min(E, elo + perE);
   // Tall tiles first, then the short ones (mixed tables): the GEMM's
@@ -161,25 +169,53 @@ __device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int
     if (c > 0 && c <= shrt) ++ns;
     else nt += (c + tall - 1) / tall;
   }
-  __shared__ int32_t s_tall_total;
+  __shared__ int32_t s_tall_total, s_short_total;
   int32_t t = block_excl_scan(nt, wsum);
   if (tid == (int)blockDim.x - 1) s_tall_total = t + nt;
   int32_t ts = block_excl_scan(ns, wsum);  // its barriers also publish s_tall_total
-  ts += s_tall_total;
+  if (blk == 0) {
+    ts += s_tall_total;
+    for (int e = elo; e < ehi; ++e) {
+      const int32_t c = s_off[e + 1] - s_off[e];
+      if (c > 0 && c <= shrt) {
+        tile_expert[ts] = e | kShortTile;
+        tile_mstart[ts] = s_off[e];
+        ++ts;
+        continue;
+      }
+      for (int32_t m = 0; m < c; m += tall, ++t) {
+        tile_expert[t] = e;
+        tile_mstart[t] = s_off[e] + m;
+      }
+    }
+    if (tid == (int)blockDim.x - 1) meta[0] = ts;  // the last thread's short tiles end the table
+    return;
+  }
+  if (tid == (int)blockDim.x - 1) s_short_total = ts + ns;
+  __syncthreads();
+  const int32_t nTb = (s_tall_total + blk - 1) / blk, nSb = (s_short_total + blk - 1) / blk;
+  const int32_t entries = (nTb + nSb) * blk;
+  // Final position of entry i of the tall (short) list: its block goes to
+  // 2b (2b+1) while the other list still has blocks, after them otherwise.
+  auto pos_tall = [&](int32_t i) { const int32_t b = i / blk; return (b < nSb ? 2 * b : nSb + b) * blk + i % blk; };
+  auto pos_short = [&](int32_t i) { const int32_t b = i / blk; return (b < nTb ? 2 * b + 1 : nTb + b) * blk + i % blk; };
+  for (int32_t i = tid; i < entries; i += (int)blockDim.x) tile_expert[i] = -1;  // holes stay -1
+  __syncthreads();
   for (int e = elo; e < ehi; ++e) {
     const int32_t c = s_off[e + 1] - s_off[e];
     if (c > 0 && c <= shrt) {
-      tile_expert[ts] = e | kShortTile;
-      tile_mstart[ts] = s_off[e];
-      ++ts;
+      const int32_t p = pos_short(ts++);
+      tile_expert[p] = e | kShortTile;
+      tile_mstart[p] = s_off[e];
       continue;
     }
     for (int32_t m = 0; m < c; m += tall, ++t) {
-      tile_expert[t] = e;
-      tile_mstart[t] = s_off[e] + m;
+      const int32_t p = pos_tall(t);
+      tile_expert[p] = e;
+      tile_mstart[p] = s_off[e] + m;
     }
   }
-  if (tid == (int)blockDim.x - 1) meta[0] = ts;  // the last thread's short tiles end the table
+  if (tid == 0) meta[0] = entries;
 }
 
 // The tile table alone, for routing tables built by an earlier call for a
@@ -590,6 +626,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
     }
     if (mt >= n_tiles || nt >= ntn) continue;
     const int te = tile_expert[mt];
+    if (te < 0) continue;  // a hole of an interleaved table
     const int e = te & ~kShortTile;
     const int m0 = tile_mstart[mt];
     const int mend = offsets[e + 1];
@@ -802,8 +839,15 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   const int cfg = tiles_of(CfgHuge::BM, CfgHuge::BN) >= 512 || short_experts ? 2
                   : tiles_of(CfgLarge::BM, CfgLarge::BN) >= 512              ? 1
                                                                              : 0;
-  const int bm = cfg == 2 ? CfgHuge::BM | CfgShort::BM << 12 : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
   const int bn = cfg == 2 ? CfgHuge::BN : cfg == 1 ? CfgLarge::BN : CfgSmall::BN;
+  const int obn = EPI == 1 ? bn / 2 : bn;
+  const int ntn = (int)((I + obn - 1) / obn);
+  // Mixed tables alternate tall and short tiles in blocks of one
+  // super-tile's M tiles (the kernel's SM).  The interleaved table can hold
+  // up to two partial blocks of holes, which the workspace bound
+  // (R/64 + E + 1 entries) covers once R >= 1400.
+  const int il_blk = cfg == 2 && R >= 1400 ? CfgHuge::SUPER / std::min(ntn, CfgHuge::SN_MAX) : 0;
+  const int bm = cfg == 2 ? CfgHuge::BM | CfgShort::BM << 12 | il_blk << 24 : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
   if (bm_used) *bm_used = bm;
   int rc = MOE_OK;
   if (ex.reuse_bm == 0) {
@@ -818,8 +862,6 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
     rc = check_launch("route_tiles_kernel");
   }
   if (rc) return rc;
-  const int obn = EPI == 1 ? bn / 2 : bn;
-  const int ntn = (int)((I + obn - 1) / obn);
   const uint16_t* x = static_cast<const uint16_t*>(X);
   const uint16_t* w = static_cast<const uint16_t*>(W);
   const uint16_t* w2 = static_cast<const uint16_t*>(W2);
