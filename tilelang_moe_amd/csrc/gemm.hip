@@ -32,9 +32,13 @@ constexpr int kScanThreads = 1024;
 // Tile tables may mix two tile heights: an entry of tile_expert with this
 // bit set is a short tile (the second configuration of the GEMM kernel).
 // The tile height argument `bm` of the routing kernels is then
-// tall | short << 12: experts with at most `short` rows get one short tile,
-// the others tiles of `tall` rows.
+// bm_mixed(tall, short, blk, reserve): experts with at most `short` rows get
+// one short tile, the others tiles of `tall` rows; blk and reserve order the
+// table (build_tile_table).
 constexpr int32_t kShortTile = 1 << 30;
+constexpr int bm_mixed(int tall, int shrt, int blk, int reserve) {
+  return tall | shrt << 10 | blk << 20 | reserve << 26;
+}
 // Byte offset of the grouped GEMM's nine schedule counters in the
 // workspace control block.
 constexpr size_t kGemmSchedOffset = 3072;
@@ -144,21 +148,22 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
 
 // The M-tile table for tile height bm from segment offsets already in LDS
 // (s_off[0..E], published by a barrier): expert e owns ceil(count_e / bm)
-// consecutive M tiles, or one short tile when bm = tall | short << 12 and
-// count_e <= short; meta[0] = number of table entries.  One block (any
-// size).
+// consecutive M tiles, or one short tile when bm = bm_mixed(tall, short,
+// blk, reserve) and count_e <= short; meta[0] = number of table entries.
+// One block (any size).
 //
-// With bm = tall | short << 12 | blk << 24 (blk > 0) the tall and the short
-// tiles alternate in blocks of blk entries (T S T S ..., the longer list's
-// remainder last), so that a GEMM that walks the table in super-tiles of
-// blk M tiles runs weight-streaming short tiles beside compute-heavy tall
-// ones.  A partial block that another block follows leaves holes, marked
+// With blk > 0 the tall and the short tiles alternate in blocks of blk
+// entries (T S T S ..., the longer list's remainder next), so that a GEMM
+// that walks the table in super-tiles of blk M tiles runs weight-streaming
+// short tiles beside compute-heavy tall ones; the last `reserve` short
+// blocks are kept for the end of the table, so the schedule ends on cheap
+// tiles.  A partial block that another block follows leaves holes, marked
 // tile_expert = -1.
 __device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int32_t* wsum,
                                         int32_t* __restrict__ tile_expert, int32_t* __restrict__ tile_mstart,
                                         int32_t* __restrict__ meta) {
   const int tid = threadIdx.x;
-  const int tall = bm & 0xFFF, shrt = (bm >> 12) & 0xFFF, blk = (bm >> 24) & 0x3F;
+  const int tall = bm & 0x3FF, shrt = (bm >> 10) & 0x3FF, blk = (bm >> 20) & 0x3F, reserve = (bm >> 26) & 0x1F;
   const int perE = (E + (int)blockDim.x - 1) / (int)blockDim.x;
   const int elo = std::min(E, tid * perE), ehi = std::min(E, elo + perE);
   // Tall tiles first, then the short ones (mixed tables): the GEMM's
@@ -194,11 +199,17 @@ __device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int
   if (tid == (int)blockDim.x - 1) s_short_total = ts + ns;
   __syncthreads();
   const int32_t nTb = (s_tall_total + blk - 1) / blk, nSb = (s_short_total + blk - 1) / blk;
+  const int32_t s1 = nSb > reserve ? nSb - reserve : 0;  // short blocks interleaved with the tall ones
   const int32_t entries = (nTb + nSb) * blk;
-  // Final position of entry i of the tall (short) list: its block goes to
-  // 2b (2b+1) while the other list still has blocks, after them otherwise.
-  auto pos_tall = [&](int32_t i) { const int32_t b = i / blk; return (b < nSb ? 2 * b : nSb + b) * blk + i % blk; };
-  auto pos_short = [&](int32_t i) { const int32_t b = i / blk; return (b < nTb ? 2 * b + 1 : nTb + b) * blk + i % blk; };
+  // Final position of entry i of the tall (short) list: tall block b goes to
+  // 2b while interleaved short blocks remain (b < s1), after them
+  // otherwise; short block b < s1 goes to 2b+1 while tall blocks remain;
+  // every other short block follows all tall blocks.
+  auto pos_tall = [&](int32_t i) { const int32_t b = i / blk; return (b < s1 ? 2 * b : s1 + b) * blk + i % blk; };
+  auto pos_short = [&](int32_t i) {
+    const int32_t b = i / blk;
+    return (b < s1 && b < nTb ? 2 * b + 1 : nTb + b) * blk + i % blk;
+  };
   for (int32_t i = tid; i < entries; i += (int)blockDim.x) tile_expert[i] = -1;  // holes stay -1
   __syncthreads();
   for (int e = elo; e < ehi; ++e) {
@@ -846,8 +857,12 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   // super-tile's M tiles (the kernel's SM).  The interleaved table can hold
   // up to two partial blocks of holes, which the workspace bound
   // (R/64 + E + 1 entries) covers once R >= 1400.
+  // The last round of the persistent grid (8 x SUPER items) is kept for
+  // short tiles.
   const int il_blk = cfg == 2 && R >= 1400 ? CfgHuge::SUPER / std::min(ntn, CfgHuge::SN_MAX) : 0;
-  const int bm = cfg == 2 ? CfgHuge::BM | CfgShort::BM << 12 | il_blk << 24 : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
+  const int il_reserve =
+      il_blk ? (int)std::min<int64_t>(31, (8 * CfgHuge::SUPER + (int64_t)il_blk * ntn - 1) / ((int64_t)il_blk * ntn)) : 0;
+  const int bm = cfg == 2 ? bm_mixed(CfgHuge::BM, CfgShort::BM, il_blk, il_reserve) : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
   if (bm_used) *bm_used = bm;
   int rc = MOE_OK;
   if (ex.reuse_bm == 0) {
