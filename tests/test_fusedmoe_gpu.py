@@ -157,6 +157,24 @@ def test_fusedmoe_large(cuda, T, Dh, De, Ds, E, k):
     torch.testing.assert_close(out.float(), torch_moe_ref(x, w, k, wts, ids.long()), rtol=2e-2, atol=2e-2)
 
 
+def test_fusedmoe_mixed_tile_tables(cuda):
+    """A routing skewed enough that the up GEMM takes the mixed 256/128-row
+    tile table (tall and short tiles interleaved, with holes) while the
+    down GEMM, narrower, takes another tile height and rebuilds the table
+    from the same routing."""
+    T, Dh, De, Ds, E, k = 4096, 512, 1024, 1024, 64, 8
+    x, w = _moe_weights(T, Dh, De, Ds, E, seed=7)
+    g = torch.Generator(device="cuda").manual_seed(8)
+    x[:, 0] = 4.0  # a constant input column turns router_weight[:, 0] into a per-expert bias
+    w["router_weight"][:, 0] = (torch.randn(E, generator=g, device="cuda") * 2.0).to(x.dtype)
+    out, wts, ids = K.fused_moe_routed(x, **w, n_experts_per_token=k, return_routing=True)
+    torch.cuda.synchronize()
+    counts = torch.bincount(ids.flatten().long(), minlength=E)
+    assert (counts > 256).any() and ((counts > 0) & (counts <= 128)).any()
+    check_routing(x, w["router_weight"], k, wts, ids)
+    torch.testing.assert_close(out.float(), torch_moe_ref(x, w, k, wts, ids.long()), rtol=2e-2, atol=2e-2)
+
+
 @pytest.mark.parametrize("T", [40, 600])  # split-H and unsplit router GEMM
 def test_fusedmoe_more_than_256_experts(cuda, T):
     """E > 256: the router runs as router GEMM + TopK (the fused router
