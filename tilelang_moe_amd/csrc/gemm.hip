@@ -166,8 +166,8 @@ __device__ inline void build_tile_table(const int32_t* s_off, int E, int bm, int
   const int tall = bm & 0x3FF, shrt = (bm >> 10) & 0x3FF, blk = (bm >> 20) & 0x3F, reserve = (bm >> 26) & 0x1F;
   const int perE = (E + (int)blockDim.x - 1) / (int)blockDim.x;
   const int elo = std::min(E, tid * perE), ehi = std::min(E, elo + perE);
-  // Tall tiles first, then the short ones (mixed tables): the GEMM's
-  // dynamic schedule then ends on the cheap tiles.
+  // Without interleaving (blk == 0) the tall tiles come first, then the
+  // short ones: the GEMM's dynamic schedule then ends on the cheap tiles.
   int32_t nt = 0, ns = 0;
   for (int e = elo; e < ehi; ++e) {
     const int32_t c = s_off[e + 1] - s_off[e];
