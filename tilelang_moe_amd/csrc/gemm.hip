@@ -854,12 +854,12 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   const int obn = EPI == 1 ? bn / 2 : bn;
   const int ntn = (int)((I + obn - 1) / obn);
   // Mixed tables alternate tall and short tiles in blocks of one
-  // super-tile's M tiles (the kernel's SM).  The interleaved table can hold
-  // up to two partial blocks of holes, which the workspace bound
-  // (R/64 + E + 1 entries) covers once R >= 1400.
-  // The last round of the persistent grid (8 x SUPER items) is kept for
-  // short tiles.
-  const int il_blk = cfg == 2 && R >= 1400 ? CfgHuge::SUPER / std::min(ntn, CfgHuge::SN_MAX) : 0;
+  // super-tile's M tiles (the kernel's SM).  The interleaved table holds at
+  // most R/256 + E entries plus two partial blocks of holes, which the
+  // workspace's R/64 + E + 1 entries cover when 3R/256 >= 2 blk.  The last
+  // round of the persistent grid (8 x SUPER items) is kept for short tiles.
+  const int il_cand = CfgHuge::SUPER / std::min(ntn, CfgHuge::SN_MAX);
+  const int il_blk = cfg == 2 && 3 * R >= 512 * (int64_t)il_cand ? il_cand : 0;
   const int il_reserve =
       il_blk ? (int)std::min<int64_t>(31, (8 * CfgHuge::SUPER + (int64_t)il_blk * ntn - 1) / ((int64_t)il_blk * ntn)) : 0;
   const int bm = cfg == 2 ? bm_mixed(CfgHuge::BM, CfgShort::BM, il_blk, il_reserve) : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
