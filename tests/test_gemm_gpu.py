@@ -252,6 +252,39 @@ def test_reuse_routing_matches_full_call(cuda):
         assert torch.equal(K.grouped_gemm_reuse_routing(X, W2, topk), Y2)
 
 
+# Routings of 2049 to 8192 rows over at most 14 experts, with 16-byte
+# aligned ids, take the self-routing launch, in which every workgroup derives
+# its tile's rows from the ids; a view of the same ids 8 or 4 bytes off that
+# alignment takes the routing sort and the GEMM.  Both must agree bitwise,
+# and the tables the self-routing launch writes must serve a reusing call.
+# (2048, 8193 rows and 15 experts are just outside.)
+@pytest.mark.parametrize("R,E,idt,dtype", [(8192, 8, torch.int64, torch.bfloat16),
+                                           (8192, 14, torch.int32, torch.float16),
+                                           (8191, 14, torch.int64, torch.bfloat16),
+                                           (8193, 8, torch.int64, torch.bfloat16),
+                                           (4000, 3, torch.int32, torch.bfloat16),
+                                           (2049, 1, torch.int64, torch.float16),
+                                           (2048, 8, torch.int64, torch.bfloat16),
+                                           (3001, 15, torch.int32, torch.bfloat16)])
+def test_self_routing_matches_sorted_path(cuda, R, E, idt, dtype):
+    X, W = make(R, 192, 160, E, seed=R + E, dtype=dtype)
+    g = torch.Generator().manual_seed(R * 31 + E)
+    ids = torch.randint(-1, E + 2, (R,), generator=g).to(idt)  # about 3 in E + 3 ids invalid
+    ids[: R // 3] = E // 2                                        # one crowded expert
+    buf = torch.empty(R + 1, dtype=idt, device=cuda)
+    buf[1:] = ids.to(cuda)
+    off = buf[1:]                       # not 16-byte aligned: routing sort + GEMM
+    al = ids.to(cuda)                   # aligned: self-routing when 2048 < R <= 8192 and E <= 14
+    assert al.data_ptr() % 16 == 0 and off.data_ptr() % 16 != 0
+    Ya = check_gemm(X, W, al)
+    assert torch.equal(K.grouped_gemm_reuse_routing(X, W, 1), Ya)
+    Yo = K.grouped_gemm(X, W, off)
+    assert torch.equal(Yo, Ya)
+    bad = ((al < 0) | (al >= E))
+    assert (Ya[bad] == 0).all()
+    assert (K.grouped_gemm(X, W, torch.full_like(al, E)) == 0).all()  # every row invalid
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_mixed_tile_heights(cuda, dtype):
     """Problems that take the tallest tiles mix them with short tiles: an

@@ -421,12 +421,14 @@ using CfgShort = GemmCfg<128, 256, 2, 4, 64, 3, 1>;  // 8 waves of 64x64, 144 KB
 template <typename C> struct TypeC { using type = C; };
 
 // One output tile: rows m0 .. min(m0 + BM, mend) of expert e's segment,
-// output columns n0 .. n0 + OBN.
+// output columns n0 .. n0 + OBN.  PREFILLED: the caller has put the tile's
+// routed rows in srow (-1 past the segment); m0 .. mend only bounds their
+// count.
 // EPI 0: Y = X W^T.  EPI 1 (SwiGLU): Y = silu(X Wg^T) * (X Wu^T) with W = Wg and
 // W2 = Wu, both [E, I, H]; a tile then covers BN/2 output columns, its even
 // 32-column blocks holding gate rows and its odd blocks the up rows of the
 // same output columns, so a lane holds both factors of each output element.
-template <typename T, typename Cfg, int MODE, int EPI>
+template <typename T, typename Cfg, int MODE, int EPI, bool PREFILLED = false>
 __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* __restrict__ X,
                                  const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
                                  const uint16_t* __restrict__ Wx, const uint16_t* __restrict__ W2x,
@@ -438,7 +440,8 @@ __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  for (int r = tid; r < BM; r += Cfg::THREADS) srow[r] = (m0 + r < mend) ? sorted_rows[m0 + r] : -1;
+  if constexpr (!PREFILLED)
+    for (int r = tid; r < BM; r += Cfg::THREADS) srow[r] = (m0 + r < mend) ? sorted_rows[m0 + r] : -1;
   // Expert e < E_ids reads W[e] (and W2[e]); the appended expert E_ids reads
   // Wx (and W2x).  X row of routed row r: r / topk for r < R_ids, else
   // r - R_ids + x_shift.
@@ -656,6 +659,259 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Self-routing grouped GEMM for small routings: R <= kSelfRows routed rows
+// and E <= kSelfMaxE experts, in one launch instead of the routing sort's
+// launches followed by the GEMM's.
+//
+// Every workgroup reads all R expert ids (coalesced: thread t holds the ids
+// of rows (q * 256 + t) * VEC .. + VEC - 1 of load round q, 4 bits each) and
+// derives what the sort would hand it: the per-expert row counts (hence the
+// M-tile list, experts in order, then the tiles of rows whose id is
+// invalid) and its own tile's rows.  Those are expert e's rows ranked in
+// (thread, slot) order: the block-exclusive prefix of the per-thread counts
+// of e plus the count of e in the thread's earlier slots.  Every workgroup
+// ranks alike, so the M tiles of e partition its rows; a row's result does
+// not depend on which tile holds it, so the output is bitwise that of the
+// sorted path.  Per-thread counts (at most kSelfPer = 32) are formed by SWAR
+// over the packed buckets; the wave and block sums are 16-bit fields, two
+// buckets per 32-bit word (R <= 8192), so one 32-bit wave scan serves two
+// buckets and never carries from one into the other.
+//
+// One extra workgroup (the last) writes the routing tables that the sort
+// would have written (counts, offsets, sorted_rows in stable row order, the
+// M-tile table), so a later call that reuses this workspace's routing finds
+// them; it holds rows t * kSelfPer .. t * kSelfPer + kSelfPer - 1 per thread,
+// which makes that order the (thread, slot) order.
+// ---------------------------------------------------------------------------
+constexpr int kSelfPer = 32;
+constexpr int64_t kSelfRows = 8192;  // CfgSmall's 256 threads x kSelfPer
+constexpr int kSelfMaxE = 14;  // buckets 0 .. E (E = invalid ids); 15 marks "no row"
+
+// Adds one to 8-bit field b of the pair (lo: buckets 0-7, hi: 8-14; 15 is
+// not counted).
+__device__ inline void self_count(uint64_t& lo, uint64_t& hi, uint32_t b) {
+  const uint64_t inc = (uint64_t)1 << ((b & 7) * 8);
+  lo += b < 8 ? inc : 0;
+  hi += (b >= 8 && b < 15) ? inc : 0;
+}
+
+__device__ inline uint32_t self_bucket(int64_t v, int E) { return (uint64_t)v < (uint64_t)E ? (uint32_t)v : (uint32_t)E; }
+__device__ inline uint32_t self_bucket(int32_t v, int E) { return (uint32_t)v < (uint32_t)E ? (uint32_t)v : (uint32_t)E; }
+
+// Count of bucket b among the 32 nibbles of pk.  After the XOR a nibble
+// equal to b is zero; adding 7 to the low three bits of a nibble sets its
+// bit 3 unless they are all zero, so bit 3 of the complement flags exactly
+// the zero nibbles.
+__device__ inline uint32_t self_count_of(const uint32_t (&pk)[kSelfPer / 8], uint32_t b) {
+  const uint32_t pat = 0x11111111u * b;
+  uint32_t c = 0;
+#pragma unroll
+  for (int j = 0; j < kSelfPer / 8; ++j) {
+    const uint32_t x = pk[j] ^ pat;
+    const uint32_t z = ~(((x & 0x77777777u) + 0x77777777u) | x | 0x77777777u);
+    c += (uint32_t)__builtin_popcount(z);
+  }
+  return c;
+}
+
+// Buckets of kSelfPer rows of this thread, 4 bits each (15: past R).  Slot
+// s = q * VEC + v (VEC ids per 16-byte load) holds row
+//   (q * NT + tid) * VEC + v    when STRIDED (a wave's loads are contiguous),
+//   tid * kSelfPer + s          otherwise (a thread's rows are contiguous).
+template <bool STRIDED, int NT, typename IdxT>
+__device__ inline void self_load(const IdxT* __restrict__ ids, int R, int E, int tid, uint32_t (&pk)[kSelfPer / 8]) {
+  constexpr int VEC = 16 / (int)sizeof(IdxT);
+  constexpr int NQ = kSelfPer / VEC;
+  static_assert(kSelfPer % VEC == 0 && kSelfPer % 8 == 0, "whole loads and bucket words");
+#pragma unroll
+  for (int j = 0; j < kSelfPer / 8; ++j) pk[j] = 0;
+  u32x4 v[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int base = STRIDED ? (q * NT + tid) * VEC : tid * kSelfPer + q * VEC;
+    if (base + VEC <= R) {
+      v[q] = *reinterpret_cast<const u32x4*>(ids + base);
+    } else {
+      // The last partial load: ids past R read as -1 (never counted below).
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[q][i] = 0xFFFFFFFFu;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        if (base + i < R) {
+          const IdxT id = ids[base + i];
+          if constexpr (sizeof(IdxT) == 8) {
+            v[q][2 * i] = (uint32_t)(uint64_t)id;
+            v[q][2 * i + 1] = (uint32_t)((uint64_t)id >> 32);
+          } else {
+            v[q][i] = (uint32_t)id;
+          }
+        }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int base = STRIDED ? (q * NT + tid) * VEC : tid * kSelfPer + q * VEC;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const int sl = q * VEC + i;
+      IdxT id;
+      if constexpr (sizeof(IdxT) == 8)
+        id = (IdxT)(((uint64_t)v[q][2 * i + 1] << 32) | v[q][2 * i]);
+      else
+        id = (IdxT)v[q][i];
+      const uint32_t b = base + i < R ? self_bucket(id, E) : 15u;
+      pk[sl / 8] |= b << ((sl % 8) * 4);
+    }
+  }
+}
+
+template <typename T, typename Cfg, typename IdxT, int EPI>
+__global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_selfroute_kernel(
+    const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
+    uint16_t* __restrict__ Y, int64_t H, int64_t I, int topk, int R, int E, int ntn, int share,
+    const IdxT* __restrict__ ids, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_rows, int bm, int32_t* __restrict__ tile_expert,
+    int32_t* __restrict__ tile_mstart, int32_t* __restrict__ meta) {
+  constexpr int BM = Cfg::BM, NT = Cfg::THREADS, NW = NT / kWave, PER = kSelfPer;
+  constexpr int OBN = EPI == 1 ? Cfg::BN / 2 : Cfg::BN;
+  constexpr int VEC = 16 / (int)sizeof(IdxT);
+  constexpr int NQ = PER / VEC;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  __shared__ __attribute__((aligned(16))) int32_t srow[BM + kWave];  // + one discard slot per lane
+  __shared__ uint32_t wtot[NW][8];
+  __shared__ uint32_t s_tot[8];
+  __shared__ int32_t s_off[kSelfMaxE + 3];
+  __shared__ int32_t wsum[NW];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const bool writer = (int)blockIdx.x == 8 * share;
+  // Work item of this workgroup: XCD x takes items x * share .. x * share +
+  // share - 1 (the hardware deals workgroups round-robin over the 8 XCDs),
+  // so the M tiles of one expert share its weights in one L2.
+  const int w = (int)(blockIdx.x & 7) * share + (int)(blockIdx.x >> 3);
+
+  uint32_t pk[PER / 8];
+  if (writer)
+    self_load<false, NT>(ids, R, E, tid, pk);
+  else
+    self_load<true, NT>(ids, R, E, tid, pk);
+  // Per-bucket counts of this thread's rows in 16-bit fields: word k holds
+  // buckets 2k and 2k + 1.
+  uint32_t own[8], pre[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    own[k] = 0;
+    if (2 * k <= E) own[k] = self_count_of(pk, 2 * k);
+    if (2 * k + 1 <= E) own[k] |= self_count_of(pk, 2 * k + 1) << 16;
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t incl = wave_incl_scan(own[k]);
+    pre[k] = incl - own[k];
+    if (lane == kWave - 1) wtot[wave][k] = incl;
+  }
+  lds_barrier();
+  // Block totals (and, in the writer, the per-thread prefixes) go to LDS,
+  // where a bucket's field is read with a computed address: a register
+  // array indexed by bucket would be placed in scratch memory.  The
+  // prefixes use the pipeline's stages, free until the tile starts.
+  uint32_t* s_pre = reinterpret_cast<uint32_t*>(smem);  // [8][NT]
+  static_assert(8 * NT * 4 <= BM * Cfg::BK * 2, "prefixes fit stage 0's A rows");
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const uint32_t s = wtot[v][k];
+      pre[k] += v < wave ? s : 0u;
+      t += s;
+    }
+    s_pre[k * NT + tid] = pre[k];
+    if (tid == 0) s_tot[k] = t;
+  }
+  lds_barrier();
+  auto field = [](uint32_t word, int b) { return (int)((word >> ((b & 1) * 16)) & 0xFFFFu); };
+  auto total = [&](int b) { return field(s_tot[b >> 1], b); };
+  auto prefix = [&](int b) { return field(s_pre[(b >> 1) * NT + tid], b); };
+  auto nib = [&](int sl) { return (int)((pk[sl / 8] >> ((sl % 8) * 4)) & 15u); };
+
+  if (writer) {
+    // The tables of the routing sort, for calls that reuse this routing.
+    // Thread t holds rows t * PER .. t * PER + PER - 1 here, so a row's
+    // place is its bucket's start + the thread's prefix + the count of the
+    // bucket earlier in the thread's rows.
+    if (tid <= E + 1) {
+      int32_t start = 0;
+      for (int b = 0; b < tid && b <= E; ++b) start += total(b);
+      s_off[tid] = tid == E + 1 ? R : start;
+      if (tid <= E) offsets[tid] = start;
+      if (tid < E) counts[tid] = total(tid);
+    }
+    lds_barrier();
+    build_tile_table(s_off, E, bm, wsum, tile_expert, tile_mstart, meta);
+    uint64_t rlo = 0, rhi = 0;  // running per-bucket counts of this thread's rows
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const uint32_t b = (uint32_t)nib(q);
+      if (b != 15u) {
+        const uint32_t run = (uint32_t)(((b < 8 ? rlo : rhi) >> ((b & 7) * 8)) & 0xFFu);
+        sorted_rows[s_off[b] + prefix((int)b) + (int32_t)run] = tid * PER + q;
+      }
+      self_count(rlo, rhi, b);
+    }
+    return;
+  }
+
+  // This workgroup's tile: M tile mt of the list, N tile nt.  The totals
+  // are read once into registers; the bucket loop is unrolled so that every
+  // field index is a constant.
+  const int mt = w / ntn, nt = w % ntn;
+  uint32_t tw[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) tw[k] = s_tot[k];
+  int e = -1, mloc = 0, acc = 0;
+#pragma unroll
+  for (int b = 0; b <= kSelfMaxE; ++b) {
+    const int n = b <= E ? (field(tw[b >> 1], b) + BM - 1) / BM : 0;
+    if (e < 0 && mt < acc + n) {
+      e = b;
+      mloc = (mt - acc) * BM;
+    }
+    acc += n;
+  }
+  if (e < 0) return;  // past the tile list (the grid covers an upper bound)
+  const int rows = min(BM, total(e) - mloc);
+  const int n0 = nt * OBN;
+  // The tile's rows: expert e's rows ranked in (thread, slot) order, which
+  // every workgroup of the launch shares, so the M tiles of e partition its
+  // rows.  (A row's result does not depend on which tile holds it.)
+  for (int r = tid; r < BM; r += NT) srow[r] = -1;
+  lds_barrier();
+  {
+    // Branch-free: a row outside the tile goes to the lane's discard slot.
+    int rk = prefix(e) - mloc;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const bool m = nib(q * VEC + i) == e;
+        srow[m && (unsigned)rk < (unsigned)BM ? rk : BM + lane] = (q * NT + tid) * VEC + i;
+        rk += m ? 1 : 0;
+      }
+  }
+  if (e == E) {  // rows whose id is invalid: zeros
+    __syncthreads();
+    for (int i = tid; i < BM * OBN; i += NT) {
+      const int r = srow[i / OBN];
+      const int64_t col = n0 + i % OBN;
+      if (r >= 0 && col < I) Y[(int64_t)r * I + col] = 0;
+    }
+    return;
+  }
+  gemm_tile<T, Cfg, 0, EPI, true>(smem, srow, X, W, W2, nullptr, nullptr, Y, H, I, topk, R, E, 0, nullptr, e, 0, rows,
+                                  n0);
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
 struct RoutePlan {
@@ -752,6 +1008,25 @@ static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, con
   grouped_gemm_kernel<T, Cfg, CfgS, MODE, EPI><<<dim3((unsigned)grid), Cfg::THREADS, lds, st>>>(
       x, w, w2, wx, w2x, y, H, I, topk, R, E, ntn, R_ids, E_ids, x_shift, sorted, offsets, t_exp, t_ms, meta, sched);
   return MOE_OK;
+}
+
+template <typename T, typename IdxT, int EPI>
+static int launch_selfroute(hipStream_t st, const uint16_t* x, const uint16_t* w, const uint16_t* w2, uint16_t* y,
+                            int64_t H, int64_t I, int topk, int64_t R, int E, int ntn, const IdxT* ids,
+                            int32_t* counts, int32_t* offsets, int32_t* sorted, int bm, int32_t* t_exp,
+                            int32_t* t_ms, int32_t* meta) {
+  using C = CfgSmall;
+  static_assert(C::THREADS * kSelfPer == kSelfRows, "one thread per kSelfPer rows");
+  static std::atomic<uint64_t> lds_cap_set{0};
+  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_selfroute_kernel<T, C, IdxT, EPI>,
+                              (int)C::LDS_BYTES, st));
+  // Items: an upper bound on the M tiles (every bucket may end in a partial
+  // tile) times the N tiles; one more workgroup writes the routing tables.
+  const int64_t items = ((R + C::BM - 1) / C::BM + E + 1) * ntn;
+  const int share = (int)((items + 7) / 8);
+  grouped_gemm_selfroute_kernel<T, C, IdxT, EPI><<<dim3((unsigned)(8 * share + 1)), C::THREADS, C::LDS_BYTES, st>>>(
+      x, w, w2, y, H, I, topk, (int)R, E, ntn, share, ids, counts, offsets, sorted, bm, t_exp, t_ms, meta);
+  return check_launch("grouped_gemm_selfroute_kernel");
 }
 
 }  // namespace moe
@@ -864,6 +1139,27 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
       il_blk ? (int)std::min<int64_t>(31, (8 * CfgHuge::SUPER + (int64_t)il_blk * ntn - 1) / ((int64_t)il_blk * ntn)) : 0;
   const int bm = cfg == 2 ? bm_mixed(CfgHuge::BM, CfgShort::BM, il_blk, il_reserve) : cfg == 1 ? CfgLarge::BM : CfgSmall::BM;
   if (bm_used) *bm_used = bm;
+  const uint16_t* x = static_cast<const uint16_t*>(X);
+  const uint16_t* w = static_cast<const uint16_t*>(W);
+  const uint16_t* w2 = static_cast<const uint16_t*>(W2);
+  uint16_t* y = static_cast<uint16_t*>(Y);
+  // Small routings without an appended expert that the one-workgroup sort
+  // does not take: one self-routing launch instead of the two-kernel sort
+  // and the GEMM.  (Up to 2048 rows the one-workgroup sort + GEMM measured
+  // faster: the self-routing prologue costs the same at any row count.)
+  if (cfg == 0 && ex.reuse_bm == 0 && ex.Tx == 0 && E <= kSelfMaxE && R > 2048 && R <= kSelfRows &&
+      ((uintptr_t)expert_ids & 15) == 0) {
+    auto self = [&](auto t_tag, const auto* ids) {
+      using TT = decltype(t_tag);
+      return launch_selfroute<TT, std::remove_cv_t<std::remove_pointer_t<decltype(ids)>>, EPI>(
+          st, x, w, w2, y, H, I, (int)topk, R, (int)E, ntn, ids, counts, offsets, sorted, bm, t_exp, t_ms, meta);
+    };
+    if (dtype == MOE_BF16)
+      return idx_dtype == MOE_I64 ? self(uint16_t{}, static_cast<const int64_t*>(expert_ids))
+                                  : self(uint16_t{}, static_cast<const int32_t*>(expert_ids));
+    return idx_dtype == MOE_I64 ? self(Half16{}, static_cast<const int64_t*>(expert_ids))
+                                : self(Half16{}, static_cast<const int32_t*>(expert_ids));
+  }
   int rc = MOE_OK;
   if (ex.reuse_bm == 0) {
     if (idx_dtype == MOE_I64)
@@ -877,12 +1173,8 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
     rc = check_launch("route_tiles_kernel");
   }
   if (rc) return rc;
-  const uint16_t* x = static_cast<const uint16_t*>(X);
-  const uint16_t* w = static_cast<const uint16_t*>(W);
-  const uint16_t* w2 = static_cast<const uint16_t*>(W2);
   const uint16_t* wx = static_cast<const uint16_t*>(ex.Wx);
   const uint16_t* w2x = static_cast<const uint16_t*>(ex.W2x);
-  uint16_t* y = static_cast<uint16_t*>(Y);
   // MOE_GEMM_TUNE_MODE (tuning builds only): 1 = copies only, 2 = MFMAs only.
 #ifndef MOE_GEMM_TUNE_MODE
 #define MOE_GEMM_TUNE_MODE 0
