@@ -851,11 +851,17 @@ __device__ inline void rekey_if_special(uint32_t* key, bool special) {
   }
 }
 
-// Sample key of thread tid for a row of N columns: column floor(tid*N/1024)
-// (exact key; identical in every workgroup of the row).
+// Sample key of thread tid for a row of N columns (exact key; identical in
+// every workgroup of the row): 64 runs of 16 consecutive columns, run j
+// starting at column floor(j*N/64).  A wave's 64 lanes then touch four
+// 64-byte runs (fp32) instead of 64 separate lines, so the sample takes
+// little of the CU's load bandwidth while the row loads are in flight
+// (C2: 15.15 against 15.43 us per call; runs of 4 gave 15.19).
+constexpr int kSampleRun = 16;
 template <typename T>
 __device__ inline uint32_t sample_key(const T* __restrict__ x, int N) {
-  const int c = (int)(((int64_t)threadIdx.x * N) / kSample);
+  const int j = (int)threadIdx.x / kSampleRun;
+  const int c = min(N - 1, (int)(((int64_t)j * N) / (kSample / kSampleRun)) + (int)threadIdx.x % kSampleRun);
   return key_of_bits(Elem<T>::bits(x + c));
 }
 
