@@ -803,8 +803,10 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_selfrout
     if (2 * k <= E) own[k] = self_count_of(pk, 2 * k);
     if (2 * k + 1 <= E) own[k] |= self_count_of(pk, 2 * k + 1) << 16;
   }
+  // Words past bucket E are never read: their scans are skipped.
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
+    if (2 * k > E) break;
     const uint32_t incl = wave_incl_scan(own[k]);
     pre[k] = incl - own[k];
     if (lane == kWave - 1) wtot[wave][k] = incl;
@@ -818,6 +820,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_selfrout
   static_assert(8 * NT * 4 <= BM * Cfg::BK * 2, "prefixes fit stage 0's A rows");
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
+    if (2 * k > E) break;
     uint32_t t = 0;
 #pragma unroll
     for (int v = 0; v < NW; ++v) {
