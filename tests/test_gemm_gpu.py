@@ -312,3 +312,26 @@ def test_mixed_tile_heights(cuda, dtype):
     assert (counts > 256).any() and ((counts > 0) & (counts <= 128)).any()
     X, W = make(T, H, I, E, seed=31, dtype=dtype)
     check_gemm(X, W, ids.to(cuda), topk)
+
+
+# A few routed rows (decode: at most 64 rows, H >= 512) take the K-split
+# launch: each tile's K range is split over several workgroups whose fp32
+# partials the last one sums in a fixed order.  Against the fp32 reference,
+# bitwise reproducible from call to call, with invalid ids, fp16, [T, topk]
+# ids, and the split's tables reused by a routed call.
+@pytest.mark.parametrize("T,topk,H,I,E,dtype", [(1, 2, 4096, 1792, 8, torch.bfloat16),
+                                                (8, 2, 2048, 1000, 8, torch.float16),
+                                                (32, 2, 1024, 256, 4, torch.bfloat16),
+                                                (3, 1, 520, 130, 3, torch.bfloat16),
+                                                (64, 1, 4096, 512, 2, torch.bfloat16)])
+def test_k_split_small_problems(cuda, T, topk, H, I, E, dtype):
+    X, W = make(T, H, I, E, seed=T * 7 + H, dtype=dtype)
+    g = torch.Generator().manual_seed(T + I)
+    ids = torch.randint(0, E, (T, topk), generator=g)
+    ids[0, 0] = E + 1  # one invalid id: a zero row
+    ids = ids.to(cuda)
+    Y = check_gemm(X, W, ids, topk)
+    assert (Y.view(T * topk, I)[0] == 0).all()
+    for _ in range(3):
+        assert torch.equal(K.grouped_gemm(X, W, ids), Y)
+    assert torch.equal(K.grouped_gemm_reuse_routing(X, W, topk), Y)

@@ -428,13 +428,28 @@ template <typename C> struct TypeC { using type = C; };
 // W2 = Wu, both [E, I, H]; a tile then covers BN/2 output columns, its even
 // 32-column blocks holding gate rows and its odd blocks the up rows of the
 // same output columns, so a lane holds both factors of each output element.
-template <typename T, typename Cfg, int MODE, int EPI, bool PREFILLED = false>
+// A K split of one output tile (gemm_tile with SPLIT): this workgroup
+// computes k in [kb, ke) only, publishes its fp32 partial tile, and the last
+// of the S workgroups of the tile to count in sums the S partials in split
+// order (so the result does not depend on which finished last) and stores
+// the tile.  cnt[tile] is zero before and after.
+// pt: the threads that publish partials, the first pt of the workgroup
+// (all, or with at most 32 rows per tile the waves of the first 32-row
+// block: the others hold zeros).
+struct SplitK {
+  float* part;
+  uint32_t* cnt;
+  int tile, sk, S, pt;
+  int64_t kb, ke;
+};
+
+template <typename T, typename Cfg, int MODE, int EPI, bool PREFILLED = false, bool SPLIT = false>
 __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* __restrict__ X,
                                  const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
                                  const uint16_t* __restrict__ Wx, const uint16_t* __restrict__ W2x,
                                  uint16_t* __restrict__ Y, int64_t H, int64_t I, int topk, int64_t R_ids, int E_ids,
                                  int64_t x_shift, const int32_t* __restrict__ sorted_rows, int e, int m0, int mend,
-                                 int n0) {
+                                 int n0, const SplitK* sp = nullptr) {
   constexpr int BM = Cfg::BM;
   static_assert(EPI == 0 || Cfg::FN % 2 == 0, "SwiGLU pairs 32-column blocks within a wave");
   const int tid = threadIdx.x;
@@ -489,7 +504,70 @@ __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* 
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  tile_mainloop<T, Cfg, MODE>(smem, a_src, b_src, 0, H, fm_act, acc);
+  if constexpr (SPLIT) {
+    tile_mainloop<T, Cfg, MODE>(smem, a_src, b_src, sp->kb, sp->ke, fm_act, acc);
+    // Publish the partial with agent-scope stores (they reach memory past
+    // this XCD's L2), wait for them, then count in.  No fence: only the
+    // counting workgroup reads them, after its count.
+    constexpr int NV = Cfg::FM * Cfg::FN * 16;
+    // Element u of thread t at [(tile * S + split) * NV + u][t]: a wave's
+    // stores and loads of one element are contiguous.
+    const int pt = sp->pt;
+    if (tid < pt) {
+      float* mine = sp->part + (size_t)(sp->tile * sp->S + sp->sk) * NV * pt + tid;
+#pragma unroll
+      for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            __hip_atomic_store(mine + ((i * Cfg::FN + j) * 16 + v) * pt, acc[i][j][v], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // every counter, vmcnt included
+    __syncthreads();
+    __shared__ int s_last;
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(sp->cnt + sp->tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (uint32_t)(sp->S - 1);
+    __syncthreads();
+    if (!s_last) return;
+    // Sum the S partials in split order (this workgroup's own from
+    // registers): each split's values are loaded together, then added.
+    f32x16 sum[Cfg::FM][Cfg::FN];
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sum[i][j][v] = 0.0f;
+    for (int q = 0; q < sp->S && tid < pt; ++q) {
+      if (q == sp->sk) {
+#pragma unroll
+        for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+          for (int j = 0; j < Cfg::FN; ++j) sum[i][j] += acc[i][j];
+        continue;
+      }
+      const float* pq = sp->part + (size_t)(sp->tile * sp->S + q) * NV * pt + tid;
+      float buf[NV];
+#pragma unroll
+      for (int u = 0; u < NV; ++u) buf[u] = __hip_atomic_load(pq + u * pt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) sum[i][j][v] += buf[(i * Cfg::FN + j) * 16 + v];
+    }
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j) acc[i][j] = sum[i][j];
+    if (tid == 0) __hip_atomic_store(sp->cnt + sp->tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    tile_mainloop<T, Cfg, MODE>(smem, a_src, b_src, 0, H, fm_act, acc);
+  }
 
   // Epilogue: accumulator v of lane l holds row 8*(v/4) + 4*(l/32) + v%4,
   // column l%32 of its 32x32 block.  Rows go back to their routed position.
@@ -523,6 +601,46 @@ __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* 
       }
     }
   }
+}
+
+// Grouped GEMM with each tile split along K over S workgroups, for problems
+// whose tiles would leave most CUs idle (a few routed rows: decode).  Items
+// 0 .. n_tiles * S - 1 are (tile, split) pairs, tile-major; the items after
+// them zero the rows whose expert id is invalid, as in the persistent kernel.
+template <typename T, typename Cfg, int EPI>
+__global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_splitk_kernel(
+    const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
+    uint16_t* __restrict__ Y, int64_t H, int64_t I, int topk, int64_t R, int E, int ntn, int S, int tiles_ub,
+    int64_t kchunk, int pt, const int32_t* __restrict__ sorted_rows, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_mstart,
+    const int32_t* __restrict__ meta, float* __restrict__ part, uint32_t* __restrict__ cnt) {
+  constexpr int BM = Cfg::BM;
+  constexpr int OBN = EPI == 1 ? Cfg::BN / 2 : Cfg::BN;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  __shared__ __attribute__((aligned(16))) int32_t srow[BM];
+  const int tid = threadIdx.x;
+  const int w = (int)blockIdx.x;
+  const int n_tiles = meta[0] * ntn;
+  if (w >= tiles_ub * S) {
+    // Zero the rows past offsets[E] (invalid ids), BM rows x OBN columns per item.
+    const int z = w - tiles_ub * S;
+    const int64_t z0 = (int64_t)offsets[E] + (int64_t)(z / ntn) * BM;
+    const int n0z = (z % ntn) * OBN;
+    for (int i = tid; i < BM * OBN; i += Cfg::THREADS) {
+      const int64_t p = z0 + i / OBN;
+      const int64_t col = n0z + i % OBN;
+      if (p < R && col < I) Y[(int64_t)sorted_rows[p] * I + col] = 0;
+    }
+    return;
+  }
+  const int tile = w / S, sk = w % S;
+  if (tile >= n_tiles) return;  // the grid covers an upper bound on the tiles
+  const int mt = tile / ntn, nt = tile % ntn;
+  const int e = tile_expert[mt];
+  const int m0 = tile_mstart[mt];
+  SplitK sp{part, cnt, tile, sk, S, pt, (int64_t)sk * kchunk, min(H, (int64_t)(sk + 1) * kchunk)};
+  gemm_tile<T, Cfg, 0, EPI, false, true>(smem, srow, X, W, W2, nullptr, nullptr, Y, H, I, topk, R, E, 0, sorted_rows,
+                                          e, m0, offsets[e + 1], nt * OBN, &sp);
 }
 
 // The persistent grouped GEMM over the tile table.  Tiles of Cfg's height,
@@ -938,8 +1056,19 @@ static size_t route_scratch_bytes(int64_t R, int64_t E) {
   return align_up((size_t)(E + 1) * route_plan(R).nb * sizeof(int32_t));
 }
 
+// K split of small problems (grouped_gemm_splitk_kernel): at most
+// kSplitRows routed rows (then every expert has one M tile of CfgSmall), at
+// most kSplitMaxTiles tiles, partial tiles in a workspace region of
+// kSplitPartBytes and per-tile counters in the control block.
+constexpr int64_t kSplitRows = 64;
+constexpr size_t kSplitPartBytes = (size_t)3 << 20;
+constexpr size_t kSplitCntOffset = 3200;
+constexpr int kSplitMaxTiles = 128;
+static_assert(kSplitCntOffset + kSplitMaxTiles * 4 <= kWsCtlBytes, "split counters fit the control block");
+static_assert(kSplitCntOffset >= kGemmSchedOffset + 9 * 4, "split counters clear of the schedule counters");
+
 struct GemmLayout {
-  size_t blockcnt, counts, offsets, sorted, tile_expert, tile_mstart, meta, total;
+  size_t blockcnt, counts, offsets, sorted, tile_expert, tile_mstart, meta, split, total;
   int64_t mt_ub;
 };
 
@@ -954,6 +1083,7 @@ static GemmLayout gemm_layout(int64_t R, int64_t E) {
   g.tile_expert = o; o += align_up(g.mt_ub * sizeof(int32_t));
   g.tile_mstart = o; o += align_up(g.mt_ub * sizeof(int32_t));
   g.meta = o; o += align_up(4 * sizeof(int32_t));
+  g.split = o; if (R <= kSplitRows) o += kSplitPartBytes;
   g.total = o;
   return g;
 }
@@ -1193,6 +1323,35 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
                                                    R_ids, (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta,
                                                    sched);
   };
+  // Few rows (decode): split each tile along K so that the weights stream
+  // through many more CUs; the per-tile sums stay in a fixed order.
+  if (cfg == 0 && ex.Tx == 0 && R <= kSplitRows && MOE_GEMM_TUNE_MODE == 0) {
+    using C = CfgSmall;
+    const int64_t nk = (H + C::BK - 1) / C::BK;
+    const int64_t tiles_ub = std::min<int64_t>(Et, R) * ntn;
+    // With at most 32 rows only the waves of the first 32-row block publish.
+    static_assert(C::FM == 1 && C::WM == 2, "the second row block is the second half of the workgroup");
+    const int pt = R <= 32 ? C::THREADS / 2 : C::THREADS;
+    const int64_t per_item = (int64_t)pt * C::FM * C::FN * 16 * sizeof(float);
+    const int64_t S = std::min<int64_t>({8, nk / 4, (int64_t)(kSplitPartBytes / per_item) / tiles_ub, 384 / tiles_ub});
+    if (S >= 2 && tiles_ub <= kSplitMaxTiles) {
+      const int64_t kchunk = (nk + S - 1) / S * C::BK;
+      float* part = reinterpret_cast<float*>(ws + g.split);
+      uint32_t* cnt = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kSplitCntOffset);
+      const unsigned grid = (unsigned)(tiles_ub * S + ntn);  // + the invalid-id rows (at most one M tile)
+      auto launch = [&](auto t_tag) {
+        using TT = decltype(t_tag);
+        static std::atomic<uint64_t> lds_cap_set{0};
+        MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_splitk_kernel<TT, C, EPI>,
+                                    (int)C::LDS_BYTES, st));
+        grouped_gemm_splitk_kernel<TT, C, EPI><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
+            x, w, w2, y, H, I, (int)topk, R, (int)Et, ntn, (int)S, (int)tiles_ub, kchunk, pt, sorted, offsets, t_exp,
+            t_ms, meta, part, cnt);
+        return check_launch("grouped_gemm_splitk_kernel");
+      };
+      return dtype == MOE_BF16 ? launch(uint16_t{}) : launch(Half16{});
+    }
+  }
   rc = cfg == 2 ? run(CfgHuge{}, TypeC<CfgShort>{}) : cfg == 1 ? run(CfgLarge{}, TypeC<void>{})
                                                               : run(CfgSmall{}, TypeC<void>{});
   if (rc) return rc;
