@@ -316,12 +316,14 @@ def test_mixed_tile_heights(cuda, dtype):
 
 # A few routed rows (decode: at most 64 rows, H >= 512) take the K-split
 # launch: each tile's K range is split over several workgroups whose fp32
-# partials the last one sums in a fixed order.  Against the fp32 reference,
+# partials the last one sums in a fixed order (rows <= 8, <= 16, <= 32 and
+# <= 64 publish partials of different sizes).  Against the fp32 reference,
 # bitwise reproducible from call to call, with invalid ids, fp16, [T, topk]
 # ids, and the split's tables reused by a routed call.
 @pytest.mark.parametrize("T,topk,H,I,E,dtype", [(1, 2, 4096, 1792, 8, torch.bfloat16),
                                                 (8, 2, 2048, 1000, 8, torch.float16),
                                                 (32, 2, 1024, 256, 4, torch.bfloat16),
+                                                (12, 2, 1024, 384, 6, torch.bfloat16),
                                                 (3, 1, 520, 130, 3, torch.bfloat16),
                                                 (64, 1, 4096, 512, 2, torch.bfloat16)])
 def test_k_split_small_problems(cuda, T, topk, H, I, E, dtype):

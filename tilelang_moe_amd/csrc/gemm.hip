@@ -435,7 +435,10 @@ template <typename C> struct TypeC { using type = C; };
 // the tile.  cnt[tile] is zero before and after.
 // pt: the threads that publish partials, the first pt of the workgroup
 // (all, or with at most 32 rows per tile the waves of the first 32-row
-// block: the others hold zeros).
+// block: the others hold zeros).  nv: accumulators published per 32x32
+// block, the template's SPLITNV (accumulator v of a lane holds row
+// 8 (v / 4) + 4 (lane / 32) + v % 4, so with at most 8 m rows per tile only
+// v < 4 m can be non-zero).
 struct SplitK {
   float* part;
   uint32_t* cnt;
@@ -443,7 +446,7 @@ struct SplitK {
   int64_t kb, ke;
 };
 
-template <typename T, typename Cfg, int MODE, int EPI, bool PREFILLED = false, bool SPLIT = false>
+template <typename T, typename Cfg, int MODE, int EPI, bool PREFILLED = false, int SPLITNV = 0>
 __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* __restrict__ X,
                                  const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
                                  const uint16_t* __restrict__ Wx, const uint16_t* __restrict__ W2x,
@@ -504,7 +507,7 @@ __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* 
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  if constexpr (SPLIT) {
+  if constexpr (SPLITNV > 0) {
     tile_mainloop<T, Cfg, MODE>(smem, a_src, b_src, sp->kb, sp->ke, fm_act, acc);
     // Publish the partial with agent-scope stores (they reach memory past
     // this XCD's L2), wait for them, then count in.  No fence: only the
@@ -513,16 +516,19 @@ __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* 
     // Element u of thread t at [(tile * S + split) * NV + u][t]: a wave's
     // stores and loads of one element are contiguous.
     const int pt = sp->pt;
+    constexpr int nv = SPLITNV;
+    constexpr int NP = Cfg::FM * Cfg::FN * nv;  // published values per thread
     if (tid < pt) {
-      float* mine = sp->part + (size_t)(sp->tile * sp->S + sp->sk) * NV * pt + tid;
+      float* mine = sp->part + (size_t)(sp->tile * sp->S + sp->sk) * NP * pt + tid;
 #pragma unroll
       for (int i = 0; i < Cfg::FM; ++i)
 #pragma unroll
         for (int j = 0; j < Cfg::FN; ++j)
 #pragma unroll
           for (int v = 0; v < 16; ++v)
-            __hip_atomic_store(mine + ((i * Cfg::FN + j) * 16 + v) * pt, acc[i][j][v], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            if (v < nv)
+              __hip_atomic_store(mine + ((i * Cfg::FN + j) * nv + v) * pt, acc[i][j][v], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_s_waitcnt(0);  // every counter, vmcnt included
     __syncthreads();
@@ -549,10 +555,18 @@ __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* 
           for (int j = 0; j < Cfg::FN; ++j) sum[i][j] += acc[i][j];
         continue;
       }
-      const float* pq = sp->part + (size_t)(sp->tile * sp->S + q) * NV * pt + tid;
+      const float* pq = sp->part + (size_t)(sp->tile * sp->S + q) * NP * pt + tid;
       float buf[NV];
 #pragma unroll
-      for (int u = 0; u < NV; ++u) buf[u] = __hip_atomic_load(pq + u * pt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            buf[(i * Cfg::FN + j) * 16 + v] =
+                v < nv ? __hip_atomic_load(pq + ((i * Cfg::FN + j) * nv + v) * pt, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT)
+                       : 0.0f;
 #pragma unroll
       for (int i = 0; i < Cfg::FM; ++i)
 #pragma unroll
@@ -607,7 +621,7 @@ __device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* 
 // whose tiles would leave most CUs idle (a few routed rows: decode).  Items
 // 0 .. n_tiles * S - 1 are (tile, split) pairs, tile-major; the items after
 // them zero the rows whose expert id is invalid, as in the persistent kernel.
-template <typename T, typename Cfg, int EPI>
+template <typename T, typename Cfg, int EPI, int NVP>
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_splitk_kernel(
     const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
     uint16_t* __restrict__ Y, int64_t H, int64_t I, int topk, int64_t R, int E, int ntn, int S, int tiles_ub,
@@ -639,7 +653,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_splitk_k
   const int e = tile_expert[mt];
   const int m0 = tile_mstart[mt];
   SplitK sp{part, cnt, tile, sk, S, pt, (int64_t)sk * kchunk, min(H, (int64_t)(sk + 1) * kchunk)};
-  gemm_tile<T, Cfg, 0, EPI, false, true>(smem, srow, X, W, W2, nullptr, nullptr, Y, H, I, topk, R, E, 0, sorted_rows,
+  gemm_tile<T, Cfg, 0, EPI, false, NVP>(smem, srow, X, W, W2, nullptr, nullptr, Y, H, I, topk, R, E, 0, sorted_rows,
                                           e, m0, offsets[e + 1], nt * OBN, &sp);
 }
 
@@ -1332,24 +1346,29 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
     // With at most 32 rows only the waves of the first 32-row block publish.
     static_assert(C::FM == 1 && C::WM == 2, "the second row block is the second half of the workgroup");
     const int pt = R <= 32 ? C::THREADS / 2 : C::THREADS;
-    const int64_t per_item = (int64_t)pt * C::FM * C::FN * 16 * sizeof(float);
-    const int64_t S = std::min<int64_t>({8, nk / 4, (int64_t)(kSplitPartBytes / per_item) / tiles_ub, 384 / tiles_ub});
+    const int nv = R <= 8 ? 4 : R <= 16 ? 8 : 16;  // accumulators that can hold a row
+    const int64_t per_item = (int64_t)pt * C::FM * C::FN * nv * sizeof(float);
+    const int64_t S = std::min<int64_t>({6, nk / 4, (int64_t)(kSplitPartBytes / per_item) / tiles_ub, 384 / tiles_ub});
     if (S >= 2 && tiles_ub <= kSplitMaxTiles) {
       const int64_t kchunk = (nk + S - 1) / S * C::BK;
       float* part = reinterpret_cast<float*>(ws + g.split);
       uint32_t* cnt = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kSplitCntOffset);
       const unsigned grid = (unsigned)(tiles_ub * S + ntn);  // + the invalid-id rows (at most one M tile)
-      auto launch = [&](auto t_tag) {
+      auto launch = [&](auto t_tag, auto nv_tag) {
         using TT = decltype(t_tag);
+        constexpr int NVP = decltype(nv_tag)::value;
         static std::atomic<uint64_t> lds_cap_set{0};
-        MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_splitk_kernel<TT, C, EPI>,
+        MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_splitk_kernel<TT, C, EPI, NVP>,
                                     (int)C::LDS_BYTES, st));
-        grouped_gemm_splitk_kernel<TT, C, EPI><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
+        grouped_gemm_splitk_kernel<TT, C, EPI, NVP><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
             x, w, w2, y, H, I, (int)topk, R, (int)Et, ntn, (int)S, (int)tiles_ub, kchunk, pt, sorted, offsets, t_exp,
             t_ms, meta, part, cnt);
         return check_launch("grouped_gemm_splitk_kernel");
       };
-      return dtype == MOE_BF16 ? launch(uint16_t{}) : launch(Half16{});
+      auto by_nv = [&](auto t_tag) {
+        return nv == 4 ? launch(t_tag, IntC<4>{}) : nv == 8 ? launch(t_tag, IntC<8>{}) : launch(t_tag, IntC<16>{});
+      };
+      return dtype == MOE_BF16 ? by_nv(uint16_t{}) : by_nv(Half16{});
     }
   }
   rc = cfg == 2 ? run(CfgHuge{}, TypeC<CfgShort>{}) : cfg == 1 ? run(CfgLarge{}, TypeC<void>{})
