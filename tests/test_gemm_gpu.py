@@ -317,7 +317,9 @@ def test_mixed_tile_heights(cuda, dtype):
 # A few routed rows (decode: at most 64 rows, H >= 512) take the K-split
 # launch: each tile's K range is split over several workgroups whose fp32
 # partials the last one sums in a fixed order (rows <= 8, <= 16, <= 32 and
-# <= 64 publish partials of different sizes).  Against the fp32 reference,
+# <= 64 publish partials of different sizes).  The full call groups the rows
+# itself (no sort launch) and writes the sort's tables, which the reusing
+# call's table-driven split then reads.  Against the fp32 reference,
 # bitwise reproducible from call to call, with invalid ids, fp16, [T, topk]
 # ids, and the split's tables reused by a routed call.
 @pytest.mark.parametrize("T,topk,H,I,E,dtype", [(1, 2, 4096, 1792, 8, torch.bfloat16),
@@ -332,6 +334,8 @@ def test_k_split_small_problems(cuda, T, topk, H, I, E, dtype):
     ids = torch.randint(0, E, (T, topk), generator=g)
     ids[0, 0] = E + 1  # one invalid id: a zero row
     ids = ids.to(cuda)
+    if dtype == torch.float16:
+        ids = ids.int()  # int32 ids
     Y = check_gemm(X, W, ids, topk)
     assert (Y.view(T * topk, I)[0] == 0).all()
     for _ in range(3):

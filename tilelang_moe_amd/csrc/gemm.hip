@@ -43,6 +43,11 @@ constexpr int bm_mixed(int tall, int shrt, int blk, int reserve) {
 // workspace control block.
 constexpr size_t kGemmSchedOffset = 3072;
 
+// MOE_GEMM_TUNE_MODE (tuning builds only): 1 = copies only, 2 = MFMAs only.
+#ifndef MOE_GEMM_TUNE_MODE
+#define MOE_GEMM_TUNE_MODE 0
+#endif
+
 // Bucket of routed row r.  Rows r < R_ids carry an expert id, valid in
 // [0, E_ids); rows r >= R_ids (an appended set, e.g. a shared expert taken
 // by every token) belong to expert E_ids.  Bucket E (the number of experts,
@@ -655,6 +660,106 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_splitk_k
   SplitK sp{part, cnt, tile, sk, S, pt, (int64_t)sk * kchunk, min(H, (int64_t)(sk + 1) * kchunk)};
   gemm_tile<T, Cfg, 0, EPI, false, NVP>(smem, srow, X, W, W2, nullptr, nullptr, Y, H, I, topk, R, E, 0, sorted_rows,
                                           e, m0, offsets[e + 1], nt * OBN, &sp);
+}
+
+// The K-split GEMM for at most 64 routed rows without a routing sort:
+// every workgroup's first wave reads the ids (one row per lane) and groups
+// the rows by bucket in ascending bucket order (wave min, ballot); group g
+// with bucket e < E is expert e's one M tile, its rows in ascending order,
+// and the tiles are the groups in order times the N tiles.  Items are as in
+// grouped_gemm_splitk_kernel; one more workgroup (the last) writes the
+// routing sort's tables for calls that reuse this routing.
+template <typename T, typename Cfg, typename IdxT, int EPI, int NVP>
+__global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_splitk_self_kernel(
+    const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
+    uint16_t* __restrict__ Y, int64_t H, int64_t I, int topk, int R, int E, int ntn, int S, int tiles_ub,
+    int64_t kchunk, int pt, const IdxT* __restrict__ ids, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_rows, int bm, int32_t* __restrict__ tile_expert,
+    int32_t* __restrict__ tile_mstart, int32_t* __restrict__ meta, float* __restrict__ part,
+    uint32_t* __restrict__ cnt) {
+  constexpr int BM = Cfg::BM;
+  static_assert(BM >= kWave, "a group's rows fit one M tile");
+  constexpr int OBN = EPI == 1 ? Cfg::BN / 2 : Cfg::BN;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  __shared__ __attribute__((aligned(16))) int32_t srow[BM];
+  __shared__ int32_t g_bucket[kWave];
+  __shared__ uint64_t g_mask[kWave];
+  __shared__ int32_t s_ng;
+  const int tid = threadIdx.x;
+  const int w = (int)blockIdx.x;
+  if (tid < kWave) {
+    int b = -1;
+    if (tid < R) {
+      const IdxT v = ids[tid];
+      b = (v >= 0 && v < (IdxT)E) ? (int)v : E;
+    }
+    uint64_t active = __ballot(b >= 0);
+    int ng = 0;
+    while (active) {
+      const uint32_t key = ((active >> tid) & 1ull) ? ~(uint32_t)b : 0u;
+      const int bv = (int)~wave_max_u32(key);  // the smallest bucket left
+      const uint64_t m = __ballot(b == bv) & active;
+      if (tid == 0) {
+        g_bucket[ng] = bv;
+        g_mask[ng] = m;
+      }
+      active &= ~m;
+      ++ng;
+    }
+    if (tid == 0) s_ng = ng;
+  }
+  __syncthreads();
+  const int ng = s_ng;
+  const bool has_bad = ng > 0 && g_bucket[ng - 1] == E;
+  const int n_exp = ng - (has_bad ? 1 : 0);
+
+  if (w == (int)gridDim.x - 1) {
+    // The routing sort's tables: segment starts, counts, sorted rows (each
+    // group's rows in order at its segment) and the M-tile table.
+    // s_off in the pipeline's LDS (this workgroup runs no tile), which keeps
+    // the kernel's static LDS small enough for two workgroups per CU.
+    static_assert((kMaxExperts + 2) * 4 <= (int)Cfg::LDS_BYTES, "segment starts fit the stages");
+    int32_t* s_off = reinterpret_cast<int32_t*>(smem);
+    __shared__ int32_t wsum[Cfg::THREADS / kWave];
+    for (int e = tid; e <= E; e += Cfg::THREADS) {
+      int32_t st = 0;
+      for (int g = 0; g < ng; ++g) st += g_bucket[g] < e ? __popcll(g_mask[g]) : 0;
+      s_off[e] = st;
+      offsets[e] = st;
+    }
+    if (tid == 0) s_off[E + 1] = R;
+    __syncthreads();
+    for (int e = tid; e < E; e += Cfg::THREADS) counts[e] = s_off[e + 1] - s_off[e];
+    if (tid < kWave)
+      for (int g = 0; g < ng; ++g) {
+        const uint64_t m = g_mask[g];
+        if ((m >> tid) & 1ull) sorted_rows[s_off[g_bucket[g]] + __popcll(m & ((1ull << tid) - 1ull))] = tid;
+      }
+    build_tile_table(s_off, E, bm, wsum, tile_expert, tile_mstart, meta);
+    return;
+  }
+  if (w >= tiles_ub * S) {
+    // Rows whose id is invalid (the last group): zeros, OBN columns per item.
+    if (!has_bad) return;
+    const uint64_t m = g_mask[ng - 1];
+    const int n0z = (w - tiles_ub * S) * OBN;
+    for (int i = tid; i < kWave * OBN; i += Cfg::THREADS) {
+      const int r = i / OBN;
+      const int64_t col = n0z + i % OBN;
+      if (((m >> r) & 1ull) && col < I) Y[(int64_t)r * I + col] = 0;
+    }
+    return;
+  }
+  const int tile = w / S, sk = w % S;
+  const int gi = tile / ntn, nt = tile % ntn;
+  if (gi >= n_exp) return;  // the grid covers an upper bound on the tiles
+  const uint64_t m = g_mask[gi];
+  for (int r = tid; r < BM; r += Cfg::THREADS) srow[r] = -1;
+  __syncthreads();
+  if (tid < kWave && ((m >> tid) & 1ull)) srow[__popcll(m & ((1ull << tid) - 1ull))] = tid;
+  SplitK sp{part, cnt, tile, sk, S, pt, (int64_t)sk * kchunk, min(H, (int64_t)(sk + 1) * kchunk)};
+  gemm_tile<T, Cfg, 0, EPI, true, NVP>(smem, srow, X, W, W2, nullptr, nullptr, Y, H, I, topk, R, E, 0, nullptr,
+                                        g_bucket[gi], 0, __popcll(m), nt * OBN, &sp);
 }
 
 // The persistent grouped GEMM over the tile table.  Tiles of Cfg's height,
@@ -1307,6 +1412,63 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
     return idx_dtype == MOE_I64 ? self(Half16{}, static_cast<const int64_t*>(expert_ids))
                                 : self(Half16{}, static_cast<const int32_t*>(expert_ids));
   }
+  // Few rows (decode): split each tile along K so that the weights stream
+  // through many more CUs; the per-tile sums stay in a fixed order.
+  struct {
+    int S = 0, tiles_ub = 0, pt = 0, nv = 0;
+    int64_t kchunk = 0;
+    unsigned grid = 0;
+  } split;
+  if (cfg == 0 && ex.Tx == 0 && R <= kSplitRows && MOE_GEMM_TUNE_MODE == 0) {
+    using C = CfgSmall;
+    const int64_t nk = (H + C::BK - 1) / C::BK;
+    const int64_t tiles_ub = std::min<int64_t>(Et, R) * ntn;
+    // With at most 32 rows only the waves of the first 32-row block publish.
+    static_assert(C::FM == 1 && C::WM == 2, "the second row block is the second half of the workgroup");
+    const int pt = R <= 32 ? C::THREADS / 2 : C::THREADS;
+    const int nv = R <= 8 ? 4 : R <= 16 ? 8 : 16;  // accumulators that can hold a row
+    const int64_t per_item = (int64_t)pt * C::FM * C::FN * nv * sizeof(float);
+    const int64_t S = std::min<int64_t>({6, nk / 4, (int64_t)(kSplitPartBytes / per_item) / tiles_ub, 384 / tiles_ub});
+    if (S >= 2 && tiles_ub <= kSplitMaxTiles) {
+      split.S = (int)S;
+      split.tiles_ub = (int)tiles_ub;
+      split.pt = pt;
+      split.nv = nv;
+      split.kchunk = (nk + S - 1) / S * C::BK;
+      split.grid = (unsigned)(tiles_ub * S + ntn);  // + the invalid-id rows (at most one M tile)
+    }
+  }
+  // Split calls that route themselves: no sort launch.
+  if (split.S >= 2 && ex.reuse_bm == 0) {
+    float* part = reinterpret_cast<float*>(ws + g.split);
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kSplitCntOffset);
+    const uint16_t* x0 = static_cast<const uint16_t*>(X);
+    const uint16_t* w0 = static_cast<const uint16_t*>(W);
+    const uint16_t* w20 = static_cast<const uint16_t*>(W2);
+    uint16_t* y0 = static_cast<uint16_t*>(Y);
+    auto launch = [&](auto t_tag, auto nv_tag, const auto* ids) {
+      using TT = decltype(t_tag);
+      using IT = std::remove_cv_t<std::remove_pointer_t<decltype(ids)>>;
+      using C = CfgSmall;
+      constexpr int NVP = decltype(nv_tag)::value;
+      static std::atomic<uint64_t> lds_cap_set{0};
+      MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_splitk_self_kernel<TT, C, IT, EPI, NVP>,
+                                  (int)C::LDS_BYTES, st));
+      grouped_gemm_splitk_self_kernel<TT, C, IT, EPI, NVP><<<split.grid + 1, C::THREADS, C::LDS_BYTES, st>>>(
+          x0, w0, w20, y0, H, I, (int)topk, (int)R, (int)Et, ntn, split.S, split.tiles_ub, split.kchunk, split.pt, ids,
+          counts, offsets, sorted, bm, t_exp, t_ms, meta, part, cnt);
+      return check_launch("grouped_gemm_splitk_self_kernel");
+    };
+    auto by_nv = [&](auto t_tag, const auto* ids) {
+      return split.nv == 4 ? launch(t_tag, IntC<4>{}, ids) : split.nv == 8 ? launch(t_tag, IntC<8>{}, ids)
+                                                                           : launch(t_tag, IntC<16>{}, ids);
+    };
+    auto by_idx = [&](auto t_tag) {
+      return idx_dtype == MOE_I64 ? by_nv(t_tag, static_cast<const int64_t*>(expert_ids))
+                                  : by_nv(t_tag, static_cast<const int32_t*>(expert_ids));
+    };
+    return dtype == MOE_BF16 ? by_idx(uint16_t{}) : by_idx(Half16{});
+  }
   int rc = MOE_OK;
   if (ex.reuse_bm == 0) {
     if (idx_dtype == MOE_I64)
@@ -1322,10 +1484,6 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   if (rc) return rc;
   const uint16_t* wx = static_cast<const uint16_t*>(ex.Wx);
   const uint16_t* w2x = static_cast<const uint16_t*>(ex.W2x);
-  // MOE_GEMM_TUNE_MODE (tuning builds only): 1 = copies only, 2 = MFMAs only.
-#ifndef MOE_GEMM_TUNE_MODE
-#define MOE_GEMM_TUNE_MODE 0
-#endif
   auto run = [&](auto cfg_tag, auto cfgs_tag) {
     using C = decltype(cfg_tag);
     using CS = typename decltype(cfgs_tag)::type;
@@ -1337,39 +1495,26 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
                                                    R_ids, (int)E, ex.x_shift, sorted, offsets, t_exp, t_ms, meta,
                                                    sched);
   };
-  // Few rows (decode): split each tile along K so that the weights stream
-  // through many more CUs; the per-tile sums stay in a fixed order.
-  if (cfg == 0 && ex.Tx == 0 && R <= kSplitRows && MOE_GEMM_TUNE_MODE == 0) {
-    using C = CfgSmall;
-    const int64_t nk = (H + C::BK - 1) / C::BK;
-    const int64_t tiles_ub = std::min<int64_t>(Et, R) * ntn;
-    // With at most 32 rows only the waves of the first 32-row block publish.
-    static_assert(C::FM == 1 && C::WM == 2, "the second row block is the second half of the workgroup");
-    const int pt = R <= 32 ? C::THREADS / 2 : C::THREADS;
-    const int nv = R <= 8 ? 4 : R <= 16 ? 8 : 16;  // accumulators that can hold a row
-    const int64_t per_item = (int64_t)pt * C::FM * C::FN * nv * sizeof(float);
-    const int64_t S = std::min<int64_t>({6, nk / 4, (int64_t)(kSplitPartBytes / per_item) / tiles_ub, 384 / tiles_ub});
-    if (S >= 2 && tiles_ub <= kSplitMaxTiles) {
-      const int64_t kchunk = (nk + S - 1) / S * C::BK;
-      float* part = reinterpret_cast<float*>(ws + g.split);
-      uint32_t* cnt = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kSplitCntOffset);
-      const unsigned grid = (unsigned)(tiles_ub * S + ntn);  // + the invalid-id rows (at most one M tile)
-      auto launch = [&](auto t_tag, auto nv_tag) {
-        using TT = decltype(t_tag);
-        constexpr int NVP = decltype(nv_tag)::value;
-        static std::atomic<uint64_t> lds_cap_set{0};
-        MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_splitk_kernel<TT, C, EPI, NVP>,
-                                    (int)C::LDS_BYTES, st));
-        grouped_gemm_splitk_kernel<TT, C, EPI, NVP><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
-            x, w, w2, y, H, I, (int)topk, R, (int)Et, ntn, (int)S, (int)tiles_ub, kchunk, pt, sorted, offsets, t_exp,
-            t_ms, meta, part, cnt);
-        return check_launch("grouped_gemm_splitk_kernel");
-      };
-      auto by_nv = [&](auto t_tag) {
-        return nv == 4 ? launch(t_tag, IntC<4>{}) : nv == 8 ? launch(t_tag, IntC<8>{}) : launch(t_tag, IntC<16>{});
-      };
-      return dtype == MOE_BF16 ? by_nv(uint16_t{}) : by_nv(Half16{});
-    }
+  if (split.S >= 2) {
+    float* part = reinterpret_cast<float*>(ws + g.split);
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kSplitCntOffset);
+    auto launch = [&](auto t_tag, auto nv_tag) {
+      using TT = decltype(t_tag);
+      using C = CfgSmall;
+      constexpr int NVP = decltype(nv_tag)::value;
+      static std::atomic<uint64_t> lds_cap_set{0};
+      MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_splitk_kernel<TT, C, EPI, NVP>,
+                                  (int)C::LDS_BYTES, st));
+      grouped_gemm_splitk_kernel<TT, C, EPI, NVP><<<split.grid, C::THREADS, C::LDS_BYTES, st>>>(
+          x, w, w2, y, H, I, (int)topk, R, (int)Et, ntn, split.S, split.tiles_ub, split.kchunk, split.pt, sorted,
+          offsets, t_exp, t_ms, meta, part, cnt);
+      return check_launch("grouped_gemm_splitk_kernel");
+    };
+    auto by_nv = [&](auto t_tag) {
+      return split.nv == 4 ? launch(t_tag, IntC<4>{}) : split.nv == 8 ? launch(t_tag, IntC<8>{})
+                                                                      : launch(t_tag, IntC<16>{});
+    };
+    return dtype == MOE_BF16 ? by_nv(uint16_t{}) : by_nv(Half16{});
   }
   rc = cfg == 2 ? run(CfgHuge{}, TypeC<CfgShort>{}) : cfg == 1 ? run(CfgLarge{}, TypeC<void>{})
                                                               : run(CfgSmall{}, TypeC<void>{});
