@@ -36,7 +36,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", default="", help="comma list of c1,c2,c3a,c3b,c4,c5,c5u,ep,router,moe (profiling runs)")
+    p.add_argument("--only", default="", help="comma list of c1,c2,c3a,c3b,c4,dec,c5,c5u,ep,router,moe (profiling runs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 1 GiB device-to-device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -261,6 +261,15 @@ def main():
         X = torch.randn(4096, 1024, generator=gc, device=dev).bfloat16()
         secondary["c4"] = gemm_entry("grouped_gemm bf16 T=4096 H=1024 I=256 E=8 top-2 (8192 rows)", X, W, idx, 2,
                                      cpu_calls=5, cold=True)
+        del W, X
+    if want("dec"):
+        # Decode: one and eight tokens, top-2 of 8 experts (the K-split path).
+        W, gc = gemm_weights(8, 1792, 4096)
+        for T in (1, 8):
+            idx = torch.topk(torch.randn(T, 8, generator=torch.Generator().manual_seed(T)), 2).indices.to(dev)
+            X = torch.randn(T, 4096, generator=gc, device=dev).bfloat16()
+            secondary[f"decode_t{T}"] = gemm_entry(
+                f"grouped_gemm bf16 decode T={T} H=4096 I=1792 E=8 top-2 ({2 * T} rows, K split)", X, W, idx, 2)
         del W, X
     if want("c5") or want("c5u") or want("ep"):
         W, gc = gemm_weights(256, 2048, 7168)
