@@ -46,8 +46,9 @@ def swiglu_ref(X, Wg, Wu, ids, topk=1):
 
 
 # Tile configurations: 64x128 (small), 128x256 ((16384, 2, 256, 384, 8)), 256x256 (8192, 2, 1000, 1900, 16).
-@pytest.mark.parametrize("T,topk,H,I,E", [(1, 1, 64, 32, 1), (300, 2, 520, 200, 5), (4096, 2, 1024, 256, 8),
-                                          (2048, 8, 512, 384, 64), (16384, 2, 256, 384, 8),
+# (4, 2, 1024, 256, 8): 8 rows, the K-split path.
+@pytest.mark.parametrize("T,topk,H,I,E", [(1, 1, 64, 32, 1), (4, 2, 1024, 256, 8), (300, 2, 520, 200, 5),
+                                          (4096, 2, 1024, 256, 8), (2048, 8, 512, 384, 64), (16384, 2, 256, 384, 8),
                                           (8192, 2, 1000, 1900, 16)])
 def test_grouped_gemm_swiglu(cuda, T, topk, H, I, E):
     g = torch.Generator(device="cuda").manual_seed(T + I)
