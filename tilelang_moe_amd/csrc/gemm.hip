@@ -452,7 +452,7 @@ struct SplitK {
 };
 
 template <typename T, typename Cfg, int MODE, int EPI, bool PREFILLED = false, int SPLITNV = 0>
-__device__ inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* __restrict__ X,
+__device__ __attribute__((always_inline)) inline void gemm_tile(uint16_t* smem, int32_t* srow, const uint16_t* __restrict__ X,
                                  const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
                                  const uint16_t* __restrict__ Wx, const uint16_t* __restrict__ W2x,
                                  uint16_t* __restrict__ Y, int64_t H, int64_t I, int topk, int64_t R_ids, int E_ids,
@@ -939,11 +939,12 @@ __device__ inline uint32_t self_bucket(int32_t v, int E) { return (uint32_t)v < 
 // equal to b is zero; adding 7 to the low three bits of a nibble sets its
 // bit 3 unless they are all zero, so bit 3 of the complement flags exactly
 // the zero nibbles.
-__device__ inline uint32_t self_count_of(const uint32_t (&pk)[kSelfPer / 8], uint32_t b) {
+template <int P>
+__device__ inline uint32_t self_count_of(const uint32_t (&pk)[P / 8], uint32_t b) {
   const uint32_t pat = 0x11111111u * b;
   uint32_t c = 0;
 #pragma unroll
-  for (int j = 0; j < kSelfPer / 8; ++j) {
+  for (int j = 0; j < P / 8; ++j) {
     const uint32_t x = pk[j] ^ pat;
     const uint32_t z = ~(((x & 0x77777777u) + 0x77777777u) | x | 0x77777777u);
     c += (uint32_t)__builtin_popcount(z);
@@ -955,17 +956,17 @@ __device__ inline uint32_t self_count_of(const uint32_t (&pk)[kSelfPer / 8], uin
 // s = q * VEC + v (VEC ids per 16-byte load) holds row
 //   (q * NT + tid) * VEC + v    when STRIDED (a wave's loads are contiguous),
 //   tid * kSelfPer + s          otherwise (a thread's rows are contiguous).
-template <bool STRIDED, int NT, typename IdxT>
-__device__ inline void self_load(const IdxT* __restrict__ ids, int R, int E, int tid, uint32_t (&pk)[kSelfPer / 8]) {
+template <bool STRIDED, int NT, int P, typename IdxT>
+__device__ inline void self_load(const IdxT* __restrict__ ids, int R, int E, int tid, uint32_t (&pk)[P / 8]) {
   constexpr int VEC = 16 / (int)sizeof(IdxT);
-  constexpr int NQ = kSelfPer / VEC;
-  static_assert(kSelfPer % VEC == 0 && kSelfPer % 8 == 0, "whole loads and bucket words");
+  constexpr int NQ = P / VEC;
+  static_assert(P % VEC == 0 && P % 8 == 0, "whole loads and bucket words");
 #pragma unroll
-  for (int j = 0; j < kSelfPer / 8; ++j) pk[j] = 0;
+  for (int j = 0; j < P / 8; ++j) pk[j] = 0;
   u32x4 v[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
-    const int base = STRIDED ? (q * NT + tid) * VEC : tid * kSelfPer + q * VEC;
+    const int base = STRIDED ? (q * NT + tid) * VEC : tid * P + q * VEC;
     if (base + VEC <= R) {
       v[q] = *reinterpret_cast<const u32x4*>(ids + base);
     } else {
@@ -987,7 +988,7 @@ __device__ inline void self_load(const IdxT* __restrict__ ids, int R, int E, int
   }
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
-    const int base = STRIDED ? (q * NT + tid) * VEC : tid * kSelfPer + q * VEC;
+    const int base = STRIDED ? (q * NT + tid) * VEC : tid * P + q * VEC;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
       const int sl = q * VEC + i;
@@ -1002,14 +1003,18 @@ __device__ inline void self_load(const IdxT* __restrict__ ids, int R, int E, int
   }
 }
 
-template <typename T, typename Cfg, typename IdxT, int EPI>
+template <typename T, typename Cfg, typename IdxT, int EPI, int PER>
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_selfroute_kernel(
     const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, const uint16_t* __restrict__ W2,
     uint16_t* __restrict__ Y, int64_t H, int64_t I, int topk, int R, int E, int ntn, int share,
     const IdxT* __restrict__ ids, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_rows, int bm, int32_t* __restrict__ tile_expert,
     int32_t* __restrict__ tile_mstart, int32_t* __restrict__ meta) {
-  constexpr int BM = Cfg::BM, NT = Cfg::THREADS, NW = NT / kWave, PER = kSelfPer;
+  constexpr int BM = Cfg::BM, NT = Cfg::THREADS, NW = NT / kWave;
+  // Tile workgroups load 32 ids per thread with coalesced (strided) loads;
+  // with 8 per thread each thread's rows are contiguous, so that a tile's
+  // rows are consecutive rows of its expert, as in the sorted path.
+  constexpr bool STRIDED = PER > 8;
   constexpr int OBN = EPI == 1 ? Cfg::BN / 2 : Cfg::BN;
   constexpr int VEC = 16 / (int)sizeof(IdxT);
   constexpr int NQ = PER / VEC;
@@ -1028,17 +1033,17 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_selfrout
 
   uint32_t pk[PER / 8];
   if (writer)
-    self_load<false, NT>(ids, R, E, tid, pk);
+    self_load<false, NT, PER>(ids, R, E, tid, pk);
   else
-    self_load<true, NT>(ids, R, E, tid, pk);
+    self_load<STRIDED, NT, PER>(ids, R, E, tid, pk);
   // Per-bucket counts of this thread's rows in 16-bit fields: word k holds
   // buckets 2k and 2k + 1.
   uint32_t own[8], pre[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     own[k] = 0;
-    if (2 * k <= E) own[k] = self_count_of(pk, 2 * k);
-    if (2 * k + 1 <= E) own[k] |= self_count_of(pk, 2 * k + 1) << 16;
+    if (2 * k <= E) own[k] = self_count_of<PER>(pk, 2 * k);
+    if (2 * k + 1 <= E) own[k] |= self_count_of<PER>(pk, 2 * k + 1) << 16;
   }
   // Words past bucket E are never read: their scans are skipped.
 #pragma unroll
@@ -1134,7 +1139,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_selfrout
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
         const bool m = nib(q * VEC + i) == e;
-        srow[m && (unsigned)rk < (unsigned)BM ? rk : BM + lane] = (q * NT + tid) * VEC + i;
+        srow[m && (unsigned)rk < (unsigned)BM ? rk : BM + lane] = STRIDED ? (q * NT + tid) * VEC + i : tid * PER + q * VEC + i;
         rk += m ? 1 : 0;
       }
   }
@@ -1262,7 +1267,7 @@ static int launch_gemm(hipStream_t st, const uint16_t* x, const uint16_t* w, con
   return MOE_OK;
 }
 
-template <typename T, typename IdxT, int EPI>
+template <typename T, typename IdxT, int EPI, int PER>
 static int launch_selfroute(hipStream_t st, const uint16_t* x, const uint16_t* w, const uint16_t* w2, uint16_t* y,
                             int64_t H, int64_t I, int topk, int64_t R, int E, int ntn, const IdxT* ids,
                             int32_t* counts, int32_t* offsets, int32_t* sorted, int bm, int32_t* t_exp,
@@ -1270,13 +1275,13 @@ static int launch_selfroute(hipStream_t st, const uint16_t* x, const uint16_t* w
   using C = CfgSmall;
   static_assert(C::THREADS * kSelfPer == kSelfRows, "one thread per kSelfPer rows");
   static std::atomic<uint64_t> lds_cap_set{0};
-  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_selfroute_kernel<T, C, IdxT, EPI>,
+  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)grouped_gemm_selfroute_kernel<T, C, IdxT, EPI, PER>,
                               (int)C::LDS_BYTES, st));
   // Items: an upper bound on the M tiles (every bucket may end in a partial
   // tile) times the N tiles; one more workgroup writes the routing tables.
   const int64_t items = ((R + C::BM - 1) / C::BM + E + 1) * ntn;
   const int share = (int)((items + 7) / 8);
-  grouped_gemm_selfroute_kernel<T, C, IdxT, EPI><<<dim3((unsigned)(8 * share + 1)), C::THREADS, C::LDS_BYTES, st>>>(
+  grouped_gemm_selfroute_kernel<T, C, IdxT, EPI, PER><<<dim3((unsigned)(8 * share + 1)), C::THREADS, C::LDS_BYTES, st>>>(
       x, w, w2, y, H, I, topk, (int)R, E, ntn, share, ids, counts, offsets, sorted, bm, t_exp, t_ms, meta);
   return check_launch("grouped_gemm_selfroute_kernel");
 }
@@ -1395,23 +1400,6 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   const uint16_t* w = static_cast<const uint16_t*>(W);
   const uint16_t* w2 = static_cast<const uint16_t*>(W2);
   uint16_t* y = static_cast<uint16_t*>(Y);
-  // Small routings without an appended expert that the one-workgroup sort
-  // does not take: one self-routing launch instead of the two-kernel sort
-  // and the GEMM.  (Up to 2048 rows the one-workgroup sort + GEMM measured
-  // faster: the self-routing prologue costs the same at any row count.)
-  if (cfg == 0 && ex.reuse_bm == 0 && ex.Tx == 0 && E <= kSelfMaxE && R > 2048 && R <= kSelfRows &&
-      ((uintptr_t)expert_ids & 15) == 0) {
-    auto self = [&](auto t_tag, const auto* ids) {
-      using TT = decltype(t_tag);
-      return launch_selfroute<TT, std::remove_cv_t<std::remove_pointer_t<decltype(ids)>>, EPI>(
-          st, x, w, w2, y, H, I, (int)topk, R, (int)E, ntn, ids, counts, offsets, sorted, bm, t_exp, t_ms, meta);
-    };
-    if (dtype == MOE_BF16)
-      return idx_dtype == MOE_I64 ? self(uint16_t{}, static_cast<const int64_t*>(expert_ids))
-                                  : self(uint16_t{}, static_cast<const int32_t*>(expert_ids));
-    return idx_dtype == MOE_I64 ? self(Half16{}, static_cast<const int64_t*>(expert_ids))
-                                : self(Half16{}, static_cast<const int32_t*>(expert_ids));
-  }
   // Few rows (decode): split each tile along K so that the weights stream
   // through many more CUs; the per-tile sums stay in a fixed order.
   struct {
@@ -1468,6 +1456,28 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
                                   : by_nv(t_tag, static_cast<const int32_t*>(expert_ids));
     };
     return dtype == MOE_BF16 ? by_idx(uint16_t{}) : by_idx(Half16{});
+  }
+  // Small routings without an appended expert (and not split): one
+  // self-routing launch instead of the routing sort's launches and the GEMM.
+  // Each thread groups kSelfPer rows above 2048 rows, 8 up to 2048.
+#ifndef MOE_SELF_MIN
+#define MOE_SELF_MIN 0
+#endif
+  if (cfg == 0 && ex.reuse_bm == 0 && ex.Tx == 0 && E <= kSelfMaxE && R > MOE_SELF_MIN && R <= kSelfRows &&
+      ((uintptr_t)expert_ids & 15) == 0) {
+    auto self = [&](auto t_tag, const auto* ids) {
+      using TT = decltype(t_tag);
+      using IT = std::remove_cv_t<std::remove_pointer_t<decltype(ids)>>;
+      return R <= 2048 ? launch_selfroute<TT, IT, EPI, 8>(st, x, w, w2, y, H, I, (int)topk, R, (int)E, ntn, ids,
+                                                           counts, offsets, sorted, bm, t_exp, t_ms, meta)
+                       : launch_selfroute<TT, IT, EPI, kSelfPer>(st, x, w, w2, y, H, I, (int)topk, R, (int)E, ntn,
+                                                                   ids, counts, offsets, sorted, bm, t_exp, t_ms, meta);
+    };
+    if (dtype == MOE_BF16)
+      return idx_dtype == MOE_I64 ? self(uint16_t{}, static_cast<const int64_t*>(expert_ids))
+                                  : self(uint16_t{}, static_cast<const int32_t*>(expert_ids));
+    return idx_dtype == MOE_I64 ? self(Half16{}, static_cast<const int64_t*>(expert_ids))
+                                : self(Half16{}, static_cast<const int32_t*>(expert_ids));
   }
   int rc = MOE_OK;
   if (ex.reuse_bm == 0) {
