@@ -109,8 +109,11 @@ def check_routing(x, router_weight, k, wts, ids):
 
 # Ds == De: the shared expert rides in the routed grouped GEMMs as expert E;
 # Ds == 2 De (two shared experts): separate shared GEMMs.
+# (4, 1024, 512, 0, 8, 2) and (3, 1024, 512, 512, 8, 2): decode-size, the
+# K-split GEMMs when no rows are appended.
 @pytest.mark.parametrize("T,Dh,De,Ds,E,k", [(64, 256, 128, 128, 8, 2), (200, 512, 256, 0, 16, 4),
-                                            (33, 1024, 512, 512, 4, 4), (48, 256, 128, 256, 8, 2)])
+                                            (33, 1024, 512, 512, 4, 4), (48, 256, 128, 256, 8, 2),
+                                            (4, 1024, 512, 0, 8, 2), (3, 1024, 512, 512, 8, 2)])
 def test_fusedmoe_vs_numpy_oracle(cuda, T, Dh, De, Ds, E, k):
     x, w = _moe_weights(T, Dh, De, Ds, E, seed=T + E)
     out, wts, ids = K.fused_moe_routed(x, **w, n_experts_per_token=k, return_routing=True)
