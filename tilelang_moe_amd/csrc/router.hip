@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void topk_select_kernel(const T* __restrict__ 
 //     compare-and-select butterflies.  Same results as topk_select_kernel.
 // ===========================================================================
 
-template <int EPL, typename IdxT>
+template <int EPL, typename IdxT, bool VEC4 = false>
 __global__ __launch_bounds__(256) void topk_select16_kernel(const uint16_t* __restrict__ logits, int64_t M, int N,
                                                             int64_t ld, int K, float* __restrict__ scores,
                                                             IdxT* __restrict__ indices) {
@@ -242,10 +242,24 @@ __global__ __launch_bounds__(256) void topk_select16_kernel(const uint16_t* __re
   uint32_t* win = win16_all + (size_t)wave * K;
   const uint16_t* x = logits + (live ? row : 0) * ld;
   uint32_t c[EPL];
+  if constexpr (VEC4) {
+    // Four consecutive columns per lane and 8-byte load (N % 4 == 0, rows
+    // 8-byte aligned): lane l holds columns 4 (l + 64 j) .. + 3.
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const int idx = lane + kWave * i;
-    c[i] = (live && idx < N) ? comp16_of(x[idx], idx) : 0u;  // 0: below every real composite
+    for (int j = 0; j < EPL / 4; ++j) {
+      const int col = 4 * (lane + kWave * j);
+      uint64_t v = 0;
+      if (live && col < N) v = *reinterpret_cast<const uint64_t*>(x + col);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        c[4 * j + t] = (live && col < N) ? comp16_of((uint16_t)(v >> (16 * t)), col + t) : 0u;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int idx = lane + kWave * i;
+      c[i] = (live && idx < N) ? comp16_of(x[idx], idx) : 0u;  // 0: below every real composite
+    }
   }
   for (int r = 0; r < K; ++r) {
     uint32_t best = c[0];
@@ -1293,6 +1307,13 @@ static void launch_select16_e(const uint16_t* x, int64_t M, int N, int64_t ld, i
                               hipStream_t st) {
   const int waves = 4;
   const int64_t grid = (M + waves - 1) / waves;
+  if constexpr (EPL % 4 == 0) {
+    if (N % 4 == 0 && ld % 4 == 0 && ((uintptr_t)x & 7) == 0) {
+      topk_select16_kernel<EPL, IdxT, true><<<dim3((unsigned)grid), dim3(waves * kWave), (size_t)waves * K * 4, st>>>(
+          x, M, N, ld, K, s, id);
+      return;
+    }
+  }
   topk_select16_kernel<EPL, IdxT><<<dim3((unsigned)grid), dim3(waves * kWave), (size_t)waves * K * 4, st>>>(
       x, M, N, ld, K, s, id);
 }
