@@ -210,6 +210,12 @@ def main():
         E, I, _ = W.shape
         R = T * topk
         calls, replays = (5, 4) if R * H * I > 1e11 else (20, 20)
+        # The large GEMMs run 15-20% slower for their first ~20 calls in a
+        # process (measured per kernel with rocprofv3); the timed calls start
+        # after that.
+        for _ in range(24 if R * H * I > 1e11 else 3):
+            K.grouped_gemm(X, W, idx)
+        torch.cuda.synchronize()
         ms_eager = gpu_time_ms(lambda: K.grouped_gemm(X, W, idx), max(5, min(args.steps, 50)),
                                min(args.warmup, 5))
         ms = graph_time_ms(lambda: K.grouped_gemm(X, W, idx), calls=calls, replays=replays)
