@@ -252,12 +252,13 @@ def test_reuse_routing_matches_full_call(cuda):
         assert torch.equal(K.grouped_gemm_reuse_routing(X, W2, topk), Y2)
 
 
-# Routings of 2049 to 8192 rows over at most 14 experts, with 16-byte
-# aligned ids, take the self-routing launch, in which every workgroup derives
-# its tile's rows from the ids; a view of the same ids 8 or 4 bytes off that
-# alignment takes the routing sort and the GEMM.  Both must agree bitwise,
-# and the tables the self-routing launch writes must serve a reusing call.
-# (2048, 8193 rows and 15 experts are just outside.)
+# Routings of up to 8192 rows over at most 14 experts, with 16-byte aligned
+# ids, take the self-routing launch (8 rows per thread up to 2048 rows, 32
+# above), in which every workgroup derives its tile's rows from the ids; a
+# view of the same ids 8 or 4 bytes off that alignment takes the routing
+# sort and the GEMM.  Both must agree bitwise, and the tables the
+# self-routing launch writes must serve a reusing call.  (8193 rows and 15
+# experts are just outside.)
 @pytest.mark.parametrize("R,E,idt,dtype", [(8192, 8, torch.int64, torch.bfloat16),
                                            (8192, 14, torch.int32, torch.float16),
                                            (8191, 14, torch.int64, torch.bfloat16),
@@ -265,6 +266,8 @@ def test_reuse_routing_matches_full_call(cuda):
                                            (4000, 3, torch.int32, torch.bfloat16),
                                            (2049, 1, torch.int64, torch.float16),
                                            (2048, 8, torch.int64, torch.bfloat16),
+                                           (1000, 14, torch.int32, torch.float16),
+                                           (100, 5, torch.int64, torch.bfloat16),
                                            (3001, 15, torch.int32, torch.bfloat16)])
 def test_self_routing_matches_sorted_path(cuda, R, E, idt, dtype):
     X, W = make(R, 192, 160, E, seed=R + E, dtype=dtype)
@@ -274,7 +277,7 @@ def test_self_routing_matches_sorted_path(cuda, R, E, idt, dtype):
     buf = torch.empty(R + 1, dtype=idt, device=cuda)
     buf[1:] = ids.to(cuda)
     off = buf[1:]                       # not 16-byte aligned: routing sort + GEMM
-    al = ids.to(cuda)                   # aligned: self-routing when 2048 < R <= 8192 and E <= 14
+    al = ids.to(cuda)                   # aligned: self-routing when R <= 8192 and E <= 14
     assert al.data_ptr() % 16 == 0 and off.data_ptr() % 16 != 0
     Ya = check_gemm(X, W, al)
     assert torch.equal(K.grouped_gemm_reuse_routing(X, W, 1), Ya)
