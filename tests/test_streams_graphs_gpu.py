@@ -29,7 +29,8 @@ def _inputs(seed):
     d["sel"] = torch.randn(256, 256, generator=g, device="cuda").bfloat16()       # selection
     d["X"] = torch.randn(512, 1024, generator=g, device="cuda").bfloat16()
     d["W"] = (0.02 * torch.randn(8, 256, 1024, generator=g, device="cuda")).bfloat16()
-    d["ids"] = torch.randint(0, 8, (512, 2), generator=g, device="cuda")
+    d["ids"] = torch.randint(0, 8, (512, 2), generator=g, device="cuda")       # 1024 rows: self-routing, 8 per thread
+    d["ids8"] = torch.randint(0, 8, (512, 8), generator=g, device="cuda")      # 4096 rows: self-routing, 32 per thread
     d["Xr"] = torch.randn(256, 2048, generator=g, device="cuda").bfloat16()
     d["Wr"] = (torch.randn(2048, 64, generator=g, device="cuda") / math.sqrt(2048)).bfloat16()
     # A weight in the kernels' layout, made once (fixed across replays, as at load time).
@@ -56,6 +57,8 @@ def _run_all(d):
     out += K.topk_softmax(d["small"], 6)
     out += K.topk_softmax(d["sel"], 8)
     out.append(K.grouped_gemm(d["X"], d["W"], d["ids"]))
+    out.append(K.grouped_gemm(d["X"], d["W"], d["ids8"]))
+    out.append(K.grouped_gemm(d["X"][:4], d["W"], d["ids"][:4]))  # 8 rows: the K split (partials, counters)
     out += K.router_topk_softmax(d["Xr"], d["Wr"], 8)
     out += K.router_topk_softmax_prepared(d["Xr"], d["Wt"], 6)
     out.append(K.fused_moe_routed(d["x"], **d["moe"], n_experts_per_token=2))
