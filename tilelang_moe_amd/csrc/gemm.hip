@@ -1019,7 +1019,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_selfrout
   constexpr int VEC = 16 / (int)sizeof(IdxT);
   constexpr int NQ = PER / VEC;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  __shared__ __attribute__((aligned(16))) int32_t srow[BM + kWave];  // + one discard slot per lane
+  __shared__ __attribute__((aligned(16))) int32_t srow[BM];
   __shared__ uint32_t wtot[NW][8];
   __shared__ uint32_t s_tot[8];
   __shared__ int32_t s_off[kSelfMaxE + 3];
@@ -1132,16 +1132,22 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MINB) void grouped_gemm_selfrout
   for (int r = tid; r < BM; r += NT) srow[r] = -1;
   lds_barrier();
   {
-    // Branch-free: a row outside the tile goes to the lane's discard slot.
+    // Only the slots holding e are visited: the SWAR zero-nibble mask of
+    // each bucket word (as in self_count_of) marks them, lowest slot first.
     int rk = prefix(e) - mloc;
+    const uint32_t pat = 0x11111111u * (uint32_t)e;
 #pragma unroll
-    for (int q = 0; q < NQ; ++q)
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        const bool m = nib(q * VEC + i) == e;
-        srow[m && (unsigned)rk < (unsigned)BM ? rk : BM + lane] = STRIDED ? (q * NT + tid) * VEC + i : tid * PER + q * VEC + i;
-        rk += m ? 1 : 0;
+    for (int j = 0; j < PER / 8; ++j) {
+      const uint32_t xw = pk[j] ^ pat;
+      uint32_t z = ~(((xw & 0x77777777u) + 0x77777777u) | xw | 0x77777777u);
+      while (z) {
+        const int sl = j * 8 + (__builtin_ctz(z) >> 2);
+        z &= z - 1u;
+        if ((unsigned)rk < (unsigned)BM)
+          srow[rk] = STRIDED ? ((sl / VEC) * NT + tid) * VEC + sl % VEC : tid * PER + sl;
+        ++rk;
       }
+    }
   }
   if (e == E) {  // rows whose id is invalid: zeros
     __syncthreads();
