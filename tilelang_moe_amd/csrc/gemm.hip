@@ -248,7 +248,7 @@ __global__ __launch_bounds__(kScanThreads) void route_tiles_kernel(const int32_t
 }
 
 // SCAN = false: blockoff holds route_scan_kernel's per-chunk prefixes and
-// offsets the segment starts.  SCAN = true (E + 1 <= kRouteThreads, so the
+// offsets the segment starts.  SCAN = true (E + 1 <= 2 kRouteThreads, so the
 // scan needs no launch of its own): blockoff holds route_count_kernel's raw
 // per-chunk counts, from which every workgroup derives the segment starts
 // and its chunk's prefixes, and workgroup 0 writes counts, offsets and the
@@ -268,26 +268,36 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
   if constexpr (SCAN) {
     int32_t* s_off = wcnt + NW * (E + 1);
     int32_t* wsum = s_off + (E + 2);
-    int32_t tot = 0, pre = 0;
-    if (tid <= E) {
-      const int32_t* row = blockoff + (int64_t)tid * nb;
+    // Thread t scans buckets 2t and 2t + 1 (E + 1 <= 2 kRouteThreads).
+    int32_t tot[2] = {0, 0}, pre[2] = {0, 0};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int bk = 2 * tid + h;
+      if (bk <= E) {
+        const int32_t* row = blockoff + (int64_t)bk * nb;
 #pragma unroll 8
-      for (int b = 0; b < nb; ++b) {
-        const int32_t c = row[b];
-        tot += c;
-        pre += b < (int)blockIdx.x ? c : 0;
+        for (int b = 0; b < nb; ++b) {
+          const int32_t c = row[b];
+          tot[h] += c;
+          pre[h] += b < (int)blockIdx.x ? c : 0;
+        }
       }
     }
-    const int32_t start = block_excl_scan(tot, wsum);
-    if (tid <= E) {
-      base[tid] = start + pre;
-      s_off[tid] = start;
+    const int32_t start0 = block_excl_scan(tot[0] + tot[1], wsum);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int bk = 2 * tid + h;
+      const int32_t start = start0 + (h ? tot[0] : 0);
+      if (bk <= E) {
+        base[bk] = start + pre[h];
+        s_off[bk] = start;
+        if (blockIdx.x == 0) {
+          offsets[bk] = start;
+          if (bk < E) counts[bk] = tot[h];
+        }
+      }
     }
     if (blockIdx.x == 0) {
-      if (tid <= E) {
-        offsets[tid] = start;
-        if (tid < E) counts[tid] = tot;
-      }
       if (tid == 0) s_off[E + 1] = (int32_t)R;
       if (bm > 0) {
         __syncthreads();
@@ -1236,7 +1246,7 @@ static int launch_route(const IdxT* ids, int64_t R, int64_t R_ids, int E_ids, in
   route_count_kernel<IdxT><<<p.nb, kRouteThreads, hist_lds, st>>>(ids, R, R_ids, E_ids, E, p.chunk, p.nb, blockcnt);
   if (int rc = check_launch("route_count_kernel")) return rc;
   const size_t scat_lds = (size_t)(E + 1) * (1 + kRouteThreads / kWave) * sizeof(int32_t);
-  if (E + 1 <= kRouteThreads) {
+  if (E + 1 <= 2 * kRouteThreads) {
     // Few buckets: each scatter workgroup scans the count table itself.
     const size_t lds = scat_lds + (size_t)(E + 2 + kRouteThreads / kWave) * sizeof(int32_t);
     route_scatter_kernel<IdxT, true><<<p.nb, kRouteThreads, lds, st>>>(
