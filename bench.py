@@ -299,6 +299,20 @@ def main():
             secondary["c5_uniform"] = gemm_entry(
                 "grouped_gemm bf16 R=32768 H=7168 I=2048 E=256 uniform (arange % 256, 128 rows per expert)",
                 X, W, ids, 1)
+            # The vendor library on the same weights and FLOPs, for scale: hipBLASLt's
+            # batched GEMM on the uniform case laid out per expert (no gather, no
+            # routing), and one dense GEMM of 32768 rows against a single expert.
+            Xb = X.view(256, 128, 7168)
+            ms_bmm = gpu_time_ms(lambda: torch.bmm(Xb, W.transpose(1, 2)), 10, 3)
+            ms_dense = gpu_time_ms(lambda: X @ W[0].T, 20, 5)
+            fl = 2.0 * 32768 * 7168 * 2048
+            secondary["c5_library"] = {
+                "workload": "torch (hipBLASLt) bf16 at the C5 FLOPs: bmm [256,128,7168]x[256,7168,2048]; "
+                            "dense [32768,7168]x[7168,2048]",
+                "ms_bmm_uniform": ms_bmm, "TFLOP_s_bmm_uniform": fl / ms_bmm / 1e9,
+                "ms_dense_one_expert": ms_dense, "TFLOP_s_dense_one_expert": fl / ms_dense / 1e9,
+                "timing": "HIP events around back-to-back calls"}
+            del Xb
         if want("ep"):
             X = torch.randn(4096, 7168, device=dev).bfloat16()
             ids = torch.arange(4096, device=dev) % 32
