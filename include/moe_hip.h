@@ -165,7 +165,8 @@ int moe_route_sort(const void* expert_ids, int idx_dtype, int64_t R, int64_t E,
  *   W           [E, I, H] row-major, same dtype, 16-byte aligned
  *   expert_ids  [T*topk], idx_dtype MOE_I32 or MOE_I64
  *   Y           [T*topk, I] row-major, same dtype as X
- *   H must be a multiple of 8.
+ *   H must be a multiple of 8; T*H and I*H at most 2^35 elements each
+ *   (64 GiB of X, or of one expert's weights); MOE_EUNSUP beyond.
  */
 int moe_grouped_gemm(const void* X, const void* W, const void* expert_ids,
                      int dtype, int idx_dtype, int64_t T, int64_t topk, int64_t H,

@@ -76,6 +76,10 @@ def test_argument_validation_without_gpu():
     assert L.moe_grouped_gemm(16, 16, 16, 0, 3, 4, 1, 16, 8, 2, 16, 16, 1 << 20, nul) == _lib.MOE_EINVAL
     assert L.moe_grouped_gemm(nul, nul, nul, 1, 3, 0, 1, 16, 8, 2, nul, nul, 0, nul) == _lib.MOE_OK
     assert L.moe_route_sort(nul, 3, 10, 0, 16, 16, 16, 16, 1 << 20, nul) == _lib.MOE_EUNSUP
+    # X, or one expert's weights, beyond 2^32 16-byte chunks (the tiles' 32-bit row offsets)
+    assert L.moe_grouped_gemm(16, 16, 16, 1, 3, 1 << 20, 1, 1 << 16, 8, 2, 16, 16, 1 << 20, nul) == _lib.MOE_EUNSUP
+    assert b"64 GiB" in L.moe_last_error()
+    assert L.moe_grouped_gemm(16, 16, 16, 1, 3, 4, 1, 1 << 16, 1 << 20, 2, 16, 16, 1 << 20, nul) == _lib.MOE_EUNSUP
 
 
 def test_python_api_rejects_cpu_tensors():

@@ -486,22 +486,28 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(uint16_t* smem, 
   // lane l fills slot l: row l / CPR, position l % CPR.
   constexpr int CPR = Cfg::CPR;
   const int crow = lane / CPR;
-  const uint16_t* a_src[Cfg::A_INS];
-  const uint16_t* b_src[Cfg::B_INS];
+  // Row offsets in 16-byte chunks (H is a multiple of 8; the host checks
+  // that X and one expert's weights span fewer than 2^32 chunks).
+  RowOffs<Cfg::A_INS> a_src;
+  a_src.base = X;
+  using BSrc = std::conditional_t<EPI == 0, RowOffs<Cfg::B_INS>, const uint16_t* [Cfg::B_INS]>;
+  BSrc b_src;
+  const int64_t hc = H / 8;
 #pragma unroll
   for (int i = 0; i < Cfg::A_INS; ++i) {
     const int r = Cfg::RPI * (wave * Cfg::A_INS + i) + crow;
     const int sr = srow[r];
     // Rows past the expert's segment read X row 0; their results are never stored.
     const int64_t xr = sr < 0 ? 0 : (sr < R_ids ? sr / topk : sr - R_ids + x_shift);
-    a_src[i] = X + xr * H + Cfg::copy_chunk(wave, i, Cfg::A_INS, lane) * 8;
+    a_src.o[i] = (uint32_t)(xr * hc + Cfg::copy_chunk(wave, i, Cfg::A_INS, lane));
   }
+  if constexpr (EPI == 0) b_src.base = We;
 #pragma unroll
   for (int i = 0; i < Cfg::B_INS; ++i) {
     const int nl = Cfg::RPI * (wave * Cfg::B_INS + i) + crow;  // tile row
     if constexpr (EPI == 0) {
       const int64_t n = n0 + nl;
-      b_src[i] = We + (n < I ? n : 0) * H + Cfg::copy_chunk(wave, i, Cfg::B_INS, lane) * 8;
+      b_src.o[i] = (uint32_t)((n < I ? n : 0) * hc + Cfg::copy_chunk(wave, i, Cfg::B_INS, lane));
     } else {
       const int blk = nl / 32;
       const int64_t n = n0 + (blk >> 1) * 32 + (nl & 31);
@@ -1362,6 +1368,9 @@ static int grouped_gemm_impl(const char* fn, const void* X, const void* W, const
   const int64_t Iv = EPI == 1 ? 2 * I : I;  // weight rows per expert the tiles walk
   if (R >= INT32_MAX || (R + kMinBM - 1) / kMinBM + Et + 1 > (int64_t)INT32_MAX / ((Iv + 63) / 64))
     return fail(MOE_EUNSUP, f + ": problem too large");
+  // The tiles address X and one expert's weights in 16-byte chunks with 32-bit offsets.
+  if (std::max(T, ex.x_shift + ex.Tx) * (H / 8) > (int64_t)UINT32_MAX || I * (H / 8) > (int64_t)UINT32_MAX)
+    return fail(MOE_EUNSUP, f + ": X or one expert's weights exceed 64 GiB");
   if (dtype != MOE_BF16 && dtype != MOE_F16)
     return fail(MOE_EINVAL, f + ": X, W and Y must be bfloat16 or float16");
   if (idx_dtype != MOE_I32 && idx_dtype != MOE_I64) return fail(MOE_EINVAL, f + ": expert ids must be int32 or int64");

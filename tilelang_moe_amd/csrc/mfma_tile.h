@@ -107,16 +107,28 @@ struct GemmCfg {
   }
 };
 
+// Copy-slot rows as 32-bit offsets, in 16-byte chunks, from one base: half
+// the registers of per-row pointers (a chunk index reaches 64 GiB past the
+// base), at one address add per copy.
+template <int N>
+struct RowOffs {
+  const uint16_t* base;
+  uint32_t o[N];
+};
+template <int N>
+__device__ inline const uint16_t* src_row(const uint16_t* const (&p)[N], int i) { return p[i]; }
+template <int N>
+__device__ inline const uint16_t* src_row(const RowOffs<N>& r, int i) { return r.base + (uint64_t)r.o[i] * 8; }
+
 // The k loop of one output tile: acc[i][j] += A-rows x B-rows over k in
 // [kb, ke) (kb a multiple of BK; elements at k >= ke count as zero).
-// a_src / b_src are this thread's copy-slot row pointers, already offset by
-// the 16-byte chunk of its slot (Cfg::copy_chunk); fm_act is the
+// a_src / b_src give this thread's copy-slot rows (pointer arrays or
+// RowOffs), already offset by the 16-byte chunk of its slot (Cfg::copy_chunk); fm_act is the
 // wave-uniform count of 32-row blocks of this wave that hold rows (the
 // MFMAs of the others are skipped).  MODE (tuning builds only): 1 = copies
 // only, 2 = MFMAs only.
-template <typename T, typename Cfg, int MODE>
-__device__ inline void tile_mainloop(uint16_t* smem, const uint16_t* const (&a_src)[Cfg::A_INS],
-                                     const uint16_t* const (&b_src)[Cfg::B_INS], int64_t kb,
+template <typename T, typename Cfg, int MODE, typename ASrc, typename BSrc>
+__device__ inline void tile_mainloop(uint16_t* smem, const ASrc& a_src, const BSrc& b_src, int64_t kb,
                                      int64_t ke, int fm_act, f32x16 (&acc)[Cfg::FM][Cfg::FN]) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, S = Cfg::STAGES, CPR = Cfg::CPR;
   constexpr int INS = Cfg::A_INS + Cfg::B_INS;
@@ -138,12 +150,12 @@ __device__ inline void tile_mainloop(uint16_t* smem, const uint16_t* const (&a_s
     auto koff = [&](int c) -> int64_t { return (!tail || k + c * 8 < ke) ? k : -(int64_t)c * 8; };
 #pragma unroll
     for (int i = 0; i < Cfg::A_INS; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + koff(Cfg::copy_chunk(wave, i, Cfg::A_INS, lane))),
+      __builtin_amdgcn_global_load_lds((const void*)(src_row(a_src, i) + koff(Cfg::copy_chunk(wave, i, Cfg::A_INS, lane))),
                                        (lds_void_t*)(st + (wave * Cfg::A_INS + i) * 512), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < Cfg::B_INS; ++i)
       __builtin_amdgcn_global_load_lds(
-          (const void*)(b_src[i] + koff(Cfg::copy_chunk(wave, i, Cfg::B_INS, lane))),
+          (const void*)(src_row(b_src, i) + koff(Cfg::copy_chunk(wave, i, Cfg::B_INS, lane))),
           (lds_void_t*)(st + BM * BK + (wave * Cfg::B_INS + i) * 512), 16, 0, 0);
   };
 
