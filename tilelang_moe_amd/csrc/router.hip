@@ -355,7 +355,7 @@ __device__ inline void radix_pick_bin(RadixState& st, const uint32_t* hist, int 
 // Same contract as radix_pick_bin with one barrier: the caller has
 // completed hist[] (barrier passed); wave 0 alone scans the 2048 bins in
 // descending order, each lane summing a block of 32, and publishes the bin
-// holding the need-th largest.
+// holding the need-th largest.  hist must be 16-byte aligned (uint4 reads).
 __device__ inline void radix_pick_bin_w0(RadixState& st, const uint32_t* hist, int sh, uint32_t dm,
                                          uint32_t* s_pick) {
   if (threadIdx.x < kWave) {
@@ -959,7 +959,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   extern __shared__ uint64_t dyn[];
   uint64_t* cand = dyn;              // [kCandCap] in extraction order
   uint64_t* tmp = dyn + kCandCap;    // [kCandCap + kOrdPad] grouped by bucket
-  __shared__ uint32_t hist[kRadixBins + 1];
+  __shared__ __align__(16) uint32_t hist[kRadixBins + 1];
   __shared__ uint32_t bstart[kOrdBuckets + 1];
   __shared__ uint32_t wsum[kRadixThreads / kWave];
   __shared__ uint32_t s_pick[3];
@@ -1102,7 +1102,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   extern __shared__ uint64_t dyn[];
   uint64_t* cand = dyn;              // [kCandCap]
   uint64_t* tmp = dyn + kCandCap;    // [kCandCap + kOrdPad]
-  __shared__ uint32_t hist[kRadixBins + 1];
+  __shared__ __align__(16) uint32_t hist[kRadixBins + 1];
   __shared__ uint32_t bstart[kOrdBuckets + 1];
   __shared__ uint32_t wsum[kRadixThreads / kWave];
   __shared__ uint32_t s_pick[3];
@@ -1198,7 +1198,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_kernel(
     const T* __restrict__ logits, int64_t M, int64_t N, int64_t ld, int K, int Kpad,
     float* __restrict__ scores, IdxT* __restrict__ indices) {
   extern __shared__ uint64_t sbuf[];  // [Kpad] winner composites
-  __shared__ uint32_t hist[kRadixBins];
+  __shared__ __align__(16) uint32_t hist[kRadixBins];
   __shared__ uint32_t wsum[kRadixThreads / kWave];
   __shared__ uint32_t s_pick[2], s_slot;
   __shared__ float s_red[kRadixThreads / kWave];
