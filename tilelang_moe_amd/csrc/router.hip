@@ -804,18 +804,18 @@ __device__ __attribute__((always_inline)) inline void order_and_store(uint64_t* 
 // into keys in place, 0 (padding) outside the range.  Keys use the plain
 // sign flip; `special` reports NaN or -0.0, for which the caller re-keys
 // with key_of_bits.
-template <typename T, int VEC, int KPT>
+template <typename T, int VEC, int KPT, bool FULL = false>
 __device__ inline void issue_row_loads(const T* __restrict__ x, int c0, int end, uint32_t* bits) {
   constexpr int NV = KPT / VEC;
   const int tid = threadIdx.x;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = c0 + VEC * (tid + kRadixThreads * j);
-    VecLoad<T, VEC>::load(x + (c + VEC <= end ? c : 0), bits + j * VEC);
+    VecLoad<T, VEC>::load(x + (FULL || c + VEC <= end ? c : 0), bits + j * VEC);
   }
 }
 
-template <typename T, int VEC, int KPT>
+template <typename T, int VEC, int KPT, bool FULL = false>
 __device__ inline void keys_from_bits(const T* __restrict__ x, int c0, int end, uint32_t* key, bool& special) {
   constexpr int NV = KPT / VEC;
   const int tid = threadIdx.x;
@@ -826,11 +826,11 @@ __device__ inline void keys_from_bits(const T* __restrict__ x, int c0, int end, 
     for (int i = 0; i < VEC; ++i) {
       const uint32_t b = key[j * VEC + i];
       special |= __builtin_amdgcn_classf(__uint_as_float(b), 0x23);  // NaN or -0
-      key[j * VEC + i] = c + VEC <= end ? key_fast(b) : 0u;
+      key[j * VEC + i] = FULL || c + VEC <= end ? key_fast(b) : 0u;
     }
   }
   // A vector straddling `end` (end - c0 not a multiple of VEC).
-  if ((end - c0) % VEC != 0) {
+  if (!FULL && (end - c0) % VEC != 0) {
     const int jt = ((end - c0) / VEC) / kRadixThreads, tt = ((end - c0) / VEC) % kRadixThreads;
     if (tid == tt && jt < NV) {
 #pragma unroll
@@ -950,7 +950,7 @@ __device__ inline void radix_row_global(const T* __restrict__ x, int64_t N, int 
 //     each candidate's column from L2 (the row was just read) instead of
 //     indexing the VGPR array dynamically.
 // ===========================================================================
-template <typename T, typename IdxT, int VEC, int KPT>
+template <typename T, typename IdxT, int VEC, int KPT, bool FULL>
 __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
     const T* __restrict__ logits, int64_t M, int N, int64_t ld, int K, int Kpad,
     float* __restrict__ scores, IdxT* __restrict__ indices) {
@@ -976,11 +976,11 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   // the row loads are still in flight.
   const uint32_t samp = sample_key(x, N);
   uint32_t key[KPT];
-  issue_row_loads<T, VEC, KPT>(x, 0, N, key);
+  issue_row_loads<T, VEC, KPT, FULL>(x, 0, N, key);
   if (tid == 0) s_max = 0;
   const uint32_t L = sample_bound(samp, K, N, hist, s_pick);  // has barriers
   bool special = false;
-  keys_from_bits<T, VEC, KPT>(x, 0, N, key, special);
+  keys_from_bits<T, VEC, KPT, FULL>(x, 0, N, key, special);
   rekey_if_special<KPT>(key, special);
   uint32_t kmax = 0;
 #pragma unroll
@@ -1408,13 +1408,18 @@ template <typename T, typename IdxT, int VEC, int KPT>
 static int launch_radix_reg(const T* x, int64_t M, int N, int64_t ld, int K, float* s, IdxT* id,
                             hipStream_t st) {
   const int Kpad = next_pow2(K);
-  static std::atomic<uint64_t> lds_cap_set{0};
-  MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)topk_radix_reg_kernel<T, IdxT, VEC, KPT>,
-                              (int)(kRadixDynLds), st));
-  topk_radix_reg_kernel<T, IdxT, VEC, KPT><<<dim3((unsigned)M), dim3(kRadixThreads),
-                                              kRadixDynLds, st>>>(x, M, N, ld, K, Kpad,
-                                                                                     s, id);
-  return check_launch("topk_radix_reg_kernel");
+  // Rows of exactly KPT keys per thread need no range checks.
+  auto go = [&](auto full) {
+    constexpr bool F = decltype(full)::value;
+    static std::atomic<uint64_t> lds_cap_set{0};
+    MOE_HIP_CHECK(lds_cap_once(lds_cap_set, (const void*)topk_radix_reg_kernel<T, IdxT, VEC, KPT, F>,
+                                (int)(kRadixDynLds), st));
+    topk_radix_reg_kernel<T, IdxT, VEC, KPT, F><<<dim3((unsigned)M), dim3(kRadixThreads), kRadixDynLds, st>>>(
+        x, M, N, ld, K, Kpad, s, id);
+    return check_launch("topk_radix_reg_kernel");
+  };
+  if (VEC > 1 && N == KPT * kRadixThreads) return go(std::true_type{});
+  return go(std::false_type{});
 }
 
 constexpr int kRadixRegMaxKPT = 32;  // keys per thread held in VGPRs
