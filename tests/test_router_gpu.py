@@ -145,6 +145,29 @@ def test_radix_adversarial_rows_full_length(cuda, k):
         check(x, k, "radix")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n", [4096, 8192, 16384, 32768])
+def test_radix_full_rows_and_neighbours(cuda, dtype, n):
+    """Rows of exactly 1024 x (keys per thread) columns take the radix
+    kernel's full-row instantiation (no per-key range checks); rows one
+    column shorter or longer take the general one.  Both, on rows with
+    NaN, -0.0 next to +0.0, ties at the K-th value and a plain row."""
+    k = min(2048, n // 4)
+    for width in (n - 1, n, n + 1):
+        g = torch.Generator(device="cpu").manual_seed(width)
+        x = torch.randn(6, width, generator=g)
+        x[0, width - 1] = float("nan")          # last column: the end of the last vector
+        x[1, :] = 0.0
+        x[1, 1::2] = -0.0
+        x[1, 7] = 1.0
+        x[2, :] = torch.randint(0, 4, (width,), generator=g).float()
+        x[3, 0] = float("inf")
+        x[4, -3:] = 6.0                         # winners in the last columns (x - max stays
+                                                # small enough for fp32 to round it within 5e-7)
+        x = x.to(dtype).to(cuda)
+        check(x, k, "radix", scores_nan_ok=True)
+
+
 @pytest.mark.parametrize("m,n,k", [(8, 40000, 100), (64, 65536, 2048), (3, 65536, 512), (17, 50000, 4096),
                                    (2, 300000, 16), (256, 32769, 64), (5, 1 << 20, 8)])
 def test_split_rows(cuda, m, n, k):

@@ -419,24 +419,58 @@ __device__ inline void lds_bitonic_desc(uint64_t* buf, int n) {
   }
 }
 
+// x * 2^48 rounded down, exactly, for x in [0, 1] (0 for NaN or x < 2^-48).
+__device__ inline uint64_t fixed48(float x) {
+  const uint32_t b = __float_as_uint(x);
+  const int e = (int)(b >> 23);                      // biased exponent (x >= 0)
+  const uint64_t m = (uint64_t)((b & 0x7FFFFFu) | 0x800000u);  // x = m 2^(e - 150)
+  const int sh = e - 102;                            // x 2^48 = m 2^sh, sh <= 25
+  if (e == 0 || e > 127) return 0;
+  return sh >= 0 ? m << sh : (sh > -24 ? m >> -sh : 0);
+}
+
+__device__ inline uint64_t wave_sum_u64(uint64_t v) {
+  v += xor_lanes_u64<1>(v);
+  v += xor_lanes_u64<2>(v);
+  v += xor_lanes_u64<4>(v);
+  v += xor_lanes_u64<8>(v);
+  v += xor_lanes_u64<16>(v);
+  v += xor_lanes_u64<32>(v);
+  return v;
+}
+
 // Softmax over buf[0..K) (descending) and the coalesced store of one row.
+// The normaliser is the same exact fixed-point sum as in order_and_store
+// (every exp in [0, 1] rounded down to a multiple of 2^-48, added as
+// uint64), so a row gets the same scores whichever path ordered it.
+// s_sum needs kRadixThreads / 64 entries.
 template <typename IdxT>
-__device__ inline void radix_epilogue(const uint64_t* buf, int K, int64_t row, float* s_red,
+__device__ inline void radix_epilogue(const uint64_t* buf, int K, int64_t row, uint64_t* s_sum,
                                       float* scores, IdxT* indices) {
   const int tid = threadIdx.x;
   const float vmax = value_of_key(comp_key(buf[0]));
-  float part = 0.0f;
-  for (int r = tid; r < K; r += kRadixThreads) part += expf(value_of_key(comp_key(buf[r])) - vmax);
-  part = wave_sum_f32(part);
-  if ((tid & (kWave - 1)) == 0) s_red[tid / kWave] = part;
+  uint64_t q = 0;
+  bool nan = false;
+  for (int r = tid; r < K; r += kRadixThreads) {
+    const float ex = expf(value_of_key(comp_key(buf[r])) - vmax);
+    q += fixed48(ex);
+    nan |= ex != ex;
+  }
+  q = wave_sum_u64(q);
+  if ((tid & (kWave - 1)) == 0) s_sum[tid / kWave] = __ballot(nan) ? ~0ull : q;
   __syncthreads();
-  float sum = 0.0f;
+  uint64_t total = 0;
+  bool any_nan = false;
 #pragma unroll
-  for (int w = 0; w < kRadixThreads / kWave; ++w) sum += s_red[w];
+  for (int w = 0; w < kRadixThreads / kWave; ++w) {
+    const uint64_t v = s_sum[w];
+    any_nan |= v == ~0ull;
+    total += v;
+  }
+  const float sum = any_nan ? __builtin_nanf("") : (float)((double)total * 0x1p-48);
   for (int r = tid; r < K; r += kRadixThreads) {
     const uint64_t w = buf[r];
-    store_out(scores, indices, row * K + r, expf(value_of_key(comp_key(w)) - vmax) / sum,
-              comp_idx(w));
+    store_out(scores, indices, row * K + r, expf(value_of_key(comp_key(w)) - vmax) / sum, comp_idx(w));
   }
 }
 
@@ -609,26 +643,6 @@ __device__ inline uint32_t sample_bound(uint32_t samp, int K, int N, uint32_t* h
   return max(ss.prefix, 1u);
 }
 
-// x * 2^48 rounded down, exactly, for x in [0, 1] (0 for NaN or x < 2^-48).
-__device__ inline uint64_t fixed48(float x) {
-  const uint32_t b = __float_as_uint(x);
-  const int e = (int)(b >> 23);                      // biased exponent (x >= 0)
-  const uint64_t m = (uint64_t)((b & 0x7FFFFFu) | 0x800000u);  // x = m 2^(e - 150)
-  const int sh = e - 102;                            // x 2^48 = m 2^sh, sh <= 25
-  if (e == 0 || e > 127) return 0;
-  return sh >= 0 ? m << sh : (sh > -24 ? m >> -sh : 0);
-}
-
-__device__ inline uint64_t wave_sum_u64(uint64_t v) {
-  v += xor_lanes_u64<1>(v);
-  v += xor_lanes_u64<2>(v);
-  v += xor_lanes_u64<4>(v);
-  v += xor_lanes_u64<8>(v);
-  v += xor_lanes_u64<16>(v);
-  v += xor_lanes_u64<32>(v);
-  return v;
-}
-
 // Clears what order_and_store expects zeroed (the bucket counts and the
 // crowding flag).  Callers run it before the barrier that publishes cand[].
 __device__ inline void order_prepare(uint32_t* hist, uint32_t* s_flag) {
@@ -646,7 +660,7 @@ __device__ inline void order_prepare(uint32_t* hist, uint32_t* s_flag) {
 template <int U, typename IdxT>
 __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t* cand, int C, uint32_t base, uint32_t rmax, int K,
                                          int64_t row, uint64_t* tmp, uint32_t* hist, uint32_t* bstart,
-                                         uint32_t* wsum, uint32_t* s_flag, float* s_red,
+                                         uint32_t* wsum, uint32_t* s_flag, uint64_t* s_red,
                                          float* scores, IdxT* indices, uint64_t* s_sum64) {
   uint32_t* s_cw = s_flag + 1;  // candidates in the buckets that can win (s_flag[2])
   constexpr int BPT = kOrdBuckets / kRadixThreads;
@@ -780,7 +794,7 @@ __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t
 template <typename IdxT>
 __device__ __attribute__((always_inline)) inline void order_and_store(uint64_t* cand, int C, uint32_t base, uint32_t rmax, int K,
                                        int64_t row, uint64_t* tmp, uint32_t* hist, uint32_t* bstart,
-                                       uint32_t* wsum, uint32_t* s_flag, float* s_red,
+                                       uint32_t* wsum, uint32_t* s_flag, uint64_t* s_red,
                                        float* scores, IdxT* indices, uint64_t* s_sum64) {
   static_assert(kCandCap == 8 * kRadixThreads, "order_and_store covers 8 candidates per thread");
   const int units = (C + kRadixThreads - 1) / kRadixThreads;
@@ -885,7 +899,7 @@ __device__ inline uint32_t sample_key(const T* __restrict__ x, int N) {
 template <typename T, typename IdxT>
 __device__ inline void radix_row_global(const T* __restrict__ x, int64_t N, int K, int Kpad, int64_t row,
                                         uint64_t* sbuf, uint32_t* hist, uint32_t* wsum, uint32_t* s_pick,
-                                        uint32_t* s_slot, float* s_red, float* scores, IdxT* indices) {
+                                        uint32_t* s_slot, uint64_t* s_red, float* scores, IdxT* indices) {
   const int tid = threadIdx.x;
   RadixState st{0u, 0u, (uint32_t)K, 0u, false};
   const int shifts[3] = {21, 10, 0};
@@ -965,7 +979,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   __shared__ uint32_t s_pick[3];
   __shared__ uint32_t s_max, s_flag[2];  // crowding flag, winner-bucket count
   __shared__ uint64_t s_sum64[kRadixThreads / kWave];
-  __shared__ float s_red[kRadixThreads / kWave];
+  __shared__ uint64_t s_red[kRadixThreads / kWave];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -1108,7 +1122,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_split_kernel(
   __shared__ uint32_t s_pick[3];
   __shared__ uint32_t s_max, s_base, s_last, s_flag[2];  // s_flag: crowding flag, winner-bucket count
   __shared__ uint64_t s_sum64[kRadixThreads / kWave];
-  __shared__ float s_red[kRadixThreads / kWave];
+  __shared__ uint64_t s_red[kRadixThreads / kWave];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -1201,7 +1215,7 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_kernel(
   __shared__ __align__(16) uint32_t hist[kRadixBins];
   __shared__ uint32_t wsum[kRadixThreads / kWave];
   __shared__ uint32_t s_pick[2], s_slot;
-  __shared__ float s_red[kRadixThreads / kWave];
+  __shared__ uint64_t s_red[kRadixThreads / kWave];
   const int64_t row = blockIdx.x;
   radix_row_global<T, IdxT>(logits + row * ld, N, K, Kpad, row, sbuf, hist, wsum, s_pick, &s_slot, s_red,
                             scores, indices);
