@@ -1009,7 +1009,8 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   uint32_t C;
   uint32_t cpos = block_excl_scan_1024((uint32_t)__popc(mask), wsum, &C);
   uint32_t base = L;
-  if (C < (uint32_t)K || C > (uint32_t)kCandCap) {
+  const bool exact = C < (uint32_t)K || C > (uint32_t)kCandCap;  // workgroup-uniform
+  if (exact) {
     // Exact threshold: radix passes over every key.  This rare path
     // re-reads the row from L2 one vector at a time so that it adds no
     // register pressure to the common path.
@@ -1074,9 +1075,24 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   const uint32_t rmax = s_max;  // complete: the scans above hold barriers
 
   // ---- extraction from the key registers (fully unrolled, no indexing) ----
+  // On the common path a slot is a candidate exactly when its key is at
+  // least L, so the test is the compare itself rather than a bit of the
+  // mask, and the slot is written through a running LDS pointer.
+  uint64_t* cp = cand + cpos;
+  if (!exact) {
+    // An opaque copy of L, so that the compiler recomputes each compare (one
+    // VALU op) instead of keeping the 32 compare masks of the candidate count
+    // alive in scalar registers, which spill.
+    uint32_t Lx;
+    asm volatile("s_mov_b32 %0, %1" : "=s"(Lx) : "s"(L));
 #pragma unroll
-  for (int i = 0; i < KPT; ++i)
-    if ((mask >> i) & 1u) cand[cpos++] = make_comp(key[i], slot_col<VEC>(0, i));
+    for (int i = 0; i < KPT; ++i)
+      if (key[i] >= Lx) *cp++ = make_comp(key[i], slot_col<VEC>(0, i));
+  } else {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i)
+      if ((mask >> i) & 1u) *cp++ = make_comp(key[i], slot_col<VEC>(0, i));
+  }
   order_prepare(hist, s_flag);
   __syncthreads();
   order_and_store(cand, (int)C, base, rmax, K, row, tmp, hist, bstart, wsum, s_flag, s_red, scores, indices,
