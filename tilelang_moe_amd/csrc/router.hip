@@ -1002,12 +1002,12 @@ __global__ __launch_bounds__(kRadixThreads) void topk_radix_reg_kernel(
   kmax = wave_max_u32(kmax);
   if (lane == 0) atomicMax(&s_max, kmax);
 
-  // ---- candidate mask: keys >= L, else exact mode ----
-  uint32_t mask = 0;
+  // ---- candidate count: keys >= L, else exact mode (which builds a mask) ----
+  uint32_t mask = 0, own = 0;
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) mask |= (uint32_t)(key[i] >= L) << i;
+  for (int i = 0; i < KPT; ++i) own += key[i] >= L;
   uint32_t C;
-  uint32_t cpos = block_excl_scan_1024((uint32_t)__popc(mask), wsum, &C);
+  uint32_t cpos = block_excl_scan_1024(own, wsum, &C);
   uint32_t base = L;
   const bool exact = C < (uint32_t)K || C > (uint32_t)kCandCap;  // workgroup-uniform
   if (exact) {
