@@ -603,18 +603,6 @@ constexpr size_t kRadixDynLds = (2 * kCandCap + kOrdPad) * sizeof(uint64_t);
 constexpr int kOrdBuckets = 2048;
 constexpr int kSample = kRadixThreads;
 
-// Histogram insert with one LDS atomic per distinct bin per wave: lanes
-// holding the same bin are found by intersecting the ballots of its bits.
-__device__ inline void wave_aggregated_add(uint32_t* hist, uint32_t bin, bool valid, int nbits) {
-  uint64_t match = __ballot(valid);
-  for (int b = 0; b < nbits; ++b) {
-    const uint64_t bal = __ballot((bin >> b) & 1u);
-    match &= ((bin >> b) & 1u) ? bal : ~bal;
-  }
-  const uint32_t lane = __lane_id();
-  if (valid && (uint32_t)(__ffsll((long long)match) - 1) == lane) atomicAdd(&hist[bin], (uint32_t)__popcll(match));
-}
-
 // Lower bound L (>= 1) on the K-th largest key of a row of N keys from one
 // sample key per thread.  Deterministic: every workgroup that passes the
 // same samples gets the same L.  hist needs kRadixBins entries.
@@ -626,7 +614,7 @@ __device__ inline uint32_t sample_bound(uint32_t samp, int K, int N, uint32_t* h
   const int tid = threadIdx.x;
   for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
   lds_barrier();
-  wave_aggregated_add(hist, samp >> 21, true, 11);
+  atomicAdd(&hist[samp >> 21], 1u);
   lds_barrier();
   RadixState ss{0u, 0u, (uint32_t)m_rank, 0u, false};
   radix_pick_bin_w0(ss, hist, 21, 0x7FFu, s_pick);
@@ -636,7 +624,7 @@ __device__ inline uint32_t sample_bound(uint32_t samp, int K, int N, uint32_t* h
     for (int b = tid; b < kRadixBins; b += kRadixThreads) hist[b] = 0;
     lds_barrier();
     const bool in = (samp & ss.fixed) == ss.prefix;
-    if (__ballot(in)) wave_aggregated_add(hist, (samp >> 10) & 0x7FFu, in, 11);
+    if (in) atomicAdd(&hist[(samp >> 10) & 0x7FFu], 1u);
     lds_barrier();
     radix_pick_bin_w0(ss, hist, 10, 0x7FFu, s_pick);
   }
