@@ -689,8 +689,7 @@ __device__ __attribute__((always_inline)) inline void order_and_store_u(uint64_t
       run += h[q];
     }
     if (tid == 0) bstart[kOrdBuckets] = (uint32_t)C;
-    hmax = wave_max_u32(hmax);
-    if (lane == 0 && hmax > (uint32_t)kBucketFixMax) *s_flag = 1;
+    if (__ballot(hmax > (uint32_t)kBucketFixMax) && lane == 0) *s_flag = 1;
   }
   __syncthreads();
   if (*s_flag) {
